@@ -1,0 +1,177 @@
+// C ABI of the token-sampling library: argument validation, launch planning and
+// error reporting.  Every check runs on the host before the first HIP call.
+#include <stdarg.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <string>
+
+#include "internal.h"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int status, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
+int fail(int status, const char *fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_last_error = buf;
+    return status;
+}
+
+int ok() {
+    g_last_error.clear();
+    return KLSAMPLE_OK;
+}
+
+size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+constexpr int32_t kMaxVocab = 1 << 24;  // masses are summed in 2^-40 fixed point in 64 bits
+
+int check_sizes(int32_t batch, int32_t vocab, int32_t dtype, int32_t max_top_k, int32_t num_logprobs) {
+    if (batch < 1 || batch > kls::kMaxBatch)
+        return fail(KLSAMPLE_ERR_INVALID_ARGUMENT, "batch must be in [1, %d] (got %d)", kls::kMaxBatch, batch);
+    if (vocab < 1 || vocab > kMaxVocab)
+        return fail(KLSAMPLE_ERR_INVALID_ARGUMENT, "vocab must be in [1, %d] (got %d)", kMaxVocab, vocab);
+    if (dtype != KLSAMPLE_FLOAT32 && dtype != KLSAMPLE_BFLOAT16)
+        return fail(KLSAMPLE_ERR_UNSUPPORTED_DTYPE, "unsupported logits dtype code %d", dtype);
+    if (max_top_k < 0) return fail(KLSAMPLE_ERR_INVALID_ARGUMENT, "max_top_k must be >= 0 (got %d)", max_top_k);
+    if (num_logprobs < 0 || num_logprobs > kls::kMaxLogprobs)
+        return fail(KLSAMPLE_ERR_INVALID_ARGUMENT, "num_logprobs must be in [0, %d] (got %d)", kls::kMaxLogprobs,
+                    num_logprobs);
+    return KLSAMPLE_OK;
+}
+
+}  // namespace
+
+namespace kls {
+
+bool make_plan(int32_t batch, int32_t vocab, int32_t dtype, int32_t max_top_k, int32_t num_logprobs, Plan *p) {
+    // Elements per thread: the largest that still gives >= 2048 workgroups (8 per CU
+    // on 256 CUs); small batches use the smallest chunks to spread a row over CUs.
+    static const int kF32[] = {32, 16, 8, 4};
+    static const int kBF16[] = {32, 16, 8};
+    const int *cands = dtype == KLSAMPLE_FLOAT32 ? kF32 : kBF16;
+    const int ncands = dtype == KLSAMPLE_FLOAT32 ? 4 : 3;
+    int e = cands[ncands - 1];
+    for (int i = 0; i < ncands; ++i) {
+        const int64_t chunk = (int64_t)kThreads * cands[i];
+        const int64_t s = (vocab + chunk - 1) / chunk;
+        if ((int64_t)batch * s >= 2048) { e = cands[i]; break; }
+    }
+    p->elems = e;
+    p->chunk = kThreads * e;
+    p->chunks = (vocab + p->chunk - 1) / p->chunk;
+    int64_t kmax = max_top_k < vocab ? max_top_k : vocab;
+    if (kmax < kTopPCandidates) kmax = kTopPCandidates;
+    if (kmax < num_logprobs) kmax = num_logprobs;
+    int64_t cap = (int64_t)align_up((size_t)(2 * kmax + 128), 64);
+    if (cap > p->chunk) cap = p->chunk;
+    p->cand_cap = (int32_t)cap;
+    const size_t B = (size_t)batch, S = (size_t)p->chunks;
+    size_t off = 0;
+    // tickets first and sized for the largest batch, so every plan finds them zero
+    p->off_tickets = off; off = align_up(off + (size_t)kMaxBatch * sizeof(uint32_t), 256);
+    p->off_stats = off;   off = align_up(off + B * S * sizeof(ChunkStat), 256);
+    p->off_cands = off;   off = align_up(off + B * S * (size_t)cap * sizeof(Cand), 256);
+    p->off_rows = off;    off = align_up(off + B * sizeof(klsample_row_info), 256);
+    p->off_ybuf = off;    off = align_up(off + B * (size_t)vocab * sizeof(float), 256);
+    p->total = off;
+    return (int64_t)batch * p->chunks <= INT32_MAX;
+}
+
+}  // namespace kls
+
+extern "C" {
+
+int klsample_abi_version(void) { return KLSAMPLE_ABI_VERSION; }
+
+const char *klsample_last_error(void) { return g_last_error.c_str(); }
+
+int klsample_workspace_size(int32_t batch, int32_t vocab, int32_t dtype, int32_t max_top_k, int32_t num_logprobs,
+                            size_t *bytes) {
+    if (bytes == nullptr) return fail(KLSAMPLE_ERR_INVALID_ARGUMENT, "bytes must not be NULL");
+    const int st = check_sizes(batch, vocab, dtype, max_top_k, num_logprobs);
+    if (st != KLSAMPLE_OK) return st;
+    kls::Plan plan;
+    if (!kls::make_plan(batch, vocab, dtype, max_top_k, num_logprobs, &plan))
+        return fail(KLSAMPLE_ERR_INVALID_ARGUMENT, "batch * chunks exceeds the grid limit");
+    *bytes = plan.total;
+    return ok();
+}
+
+int klsample_workspace_init(void *workspace, size_t workspace_bytes, void *stream) {
+    if (workspace == nullptr) return fail(KLSAMPLE_ERR_INVALID_ARGUMENT, "workspace must not be NULL");
+    if (workspace_bytes == 0) return ok();
+    const hipError_t e = kls::launch_zero_fill(workspace, workspace_bytes, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return fail(KLSAMPLE_ERR_HIP, "workspace init failed: %s", hipGetErrorString(e));
+    return ok();
+}
+
+int klsample_run(const klsample_batch *b, void *stream) {
+    if (b == nullptr) return fail(KLSAMPLE_ERR_INVALID_ARGUMENT, "batch must not be NULL");
+    int st = check_sizes(b->batch, b->vocab, b->dtype, b->max_top_k, b->num_logprobs);
+    if (st != KLSAMPLE_OK) return st;
+    if (b->logits == nullptr) return fail(KLSAMPLE_ERR_INVALID_ARGUMENT, "logits must not be NULL");
+    if (b->row_stride < b->vocab)
+        return fail(KLSAMPLE_ERR_INVALID_ARGUMENT, "row_stride (%lld) must be >= vocab (%d)",
+                    (long long)b->row_stride, b->vocab);
+    if (b->params == nullptr) return fail(KLSAMPLE_ERR_INVALID_ARGUMENT, "params must not be NULL");
+    if (b->token_ids == nullptr || b->logprobs == nullptr)
+        return fail(KLSAMPLE_ERR_INVALID_ARGUMENT, "token_ids and logprobs must not be NULL");
+    if (b->num_logprobs > 0 && (b->top_ids == nullptr || b->top_logprobs == nullptr))
+        return fail(KLSAMPLE_ERR_INVALID_ARGUMENT, "top_ids and top_logprobs are required when num_logprobs > 0");
+    if (b->history_offsets != nullptr && b->history_ids == nullptr)
+        return fail(KLSAMPLE_ERR_INVALID_ARGUMENT, "history_ids must not be NULL when history_offsets is given");
+    if ((b->options & ~(uint32_t)(KLSAMPLE_OPT_FORCE_DENSE | KLSAMPLE_OPT_SPLIT_COMBINE)) != 0)
+        return fail(KLSAMPLE_ERR_INVALID_ARGUMENT, "unknown option bits 0x%x", b->options);
+    if (b->workspace == nullptr) return fail(KLSAMPLE_ERR_WORKSPACE, "workspace must not be NULL");
+    if (((uintptr_t)b->workspace & 255u) != 0) return fail(KLSAMPLE_ERR_WORKSPACE, "workspace must be 256-byte aligned");
+    kls::Plan plan;
+    if (!kls::make_plan(b->batch, b->vocab, b->dtype, b->max_top_k, b->num_logprobs, &plan))
+        return fail(KLSAMPLE_ERR_INVALID_ARGUMENT, "batch * chunks exceeds the grid limit");
+    if (b->workspace_bytes < plan.total)
+        return fail(KLSAMPLE_ERR_WORKSPACE, "workspace too small: %zu bytes given, %zu needed", b->workspace_bytes,
+                    plan.total);
+
+    const size_t esize = b->dtype == KLSAMPLE_FLOAT32 ? 4 : 2;
+    kls::Args a;
+    a.logits = b->logits;
+    a.row_stride = b->row_stride;
+    a.B = b->batch;
+    a.V = b->vocab;
+    a.N = b->num_logprobs;
+    a.options = b->options;
+    a.params = b->params;
+    a.hist_ids = b->history_ids;
+    a.hist_off = b->history_offsets;
+    a.token = b->token_ids;
+    a.logprob = b->logprobs;
+    a.top_ids = b->top_ids;
+    a.top_lp = b->top_logprobs;
+    a.probs = b->probs;
+    a.row_info = b->row_info;
+    unsigned char *ws = static_cast<unsigned char *>(b->workspace);
+    a.tickets = reinterpret_cast<uint32_t *>(ws + plan.off_tickets);
+    a.stats = reinterpret_cast<kls::ChunkStat *>(ws + plan.off_stats);
+    a.cands = reinterpret_cast<kls::Cand *>(ws + plan.off_cands);
+    a.rows = reinterpret_cast<klsample_row_info *>(ws + plan.off_rows);
+    a.ybuf = reinterpret_cast<float *>(ws + plan.off_ybuf);
+    a.E = plan.elems;
+    a.C = plan.chunk;
+    a.S = plan.chunks;
+    a.cand_cap = plan.cand_cap;
+    a.vec_ok = (((uintptr_t)b->logits & 15u) == 0 && ((size_t)b->row_stride * esize) % 16 == 0) ? 1 : 0;
+    a.xcd_map = (b->batch % 8 == 0) ? 1 : 0;
+
+    const hipError_t e = kls::launch_sample(a, b->dtype, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return fail(KLSAMPLE_ERR_HIP, "kernel launch failed: %s", hipGetErrorString(e));
+    return ok();
+}
+
+}  // extern "C"

@@ -1,0 +1,79 @@
+// Internal declarations shared by the C ABI (api.cpp) and the gfx950 kernels (sampling.hip).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "klsample.h"
+
+namespace kls {
+
+constexpr int kThreads = 256;          // workgroup size of every kernel (4 wave64s)
+constexpr int kWaves = kThreads / 64;
+constexpr int kSortCap = 2048;         // candidates a row can resolve in LDS
+constexpr int kTopPCandidates = 64;    // per-chunk candidates for rows with top-p but no top-k
+constexpr int kMaxLogprobs = 256;      // largest supported num_logprobs
+constexpr int kMaxGroupKeys = 4096;    // group maxima examined per chunk
+constexpr int kMaxBatch = 65536;       // rows per call (sizes the ticket region)
+
+// Row classes; every row of a batch is one of these.
+enum RowMode : int { kGreedy = 0, kTopK = 1, kTopP = 2, kFull = 3 };
+
+// Per-chunk summary written by the streaming pass (32 bytes).
+struct ChunkStat {
+    float m;          // chunk max of the transformed scores (greedy / top-p / full rows)
+    int32_t arg;      // lowest index attaining m (greedy rows)
+    float y_thr;      // every element of the chunk with score >= y_thr is a candidate
+    int32_t ncand;    // candidates written (capped at the slot capacity)
+    double z;         // sum of exp(s - m) over the chunk
+    int32_t overflow; // candidates exceeded the slot capacity
+    int32_t pad;
+};
+
+struct Cand {
+    float y;          // final-space score (penalised, divided by T for sampled rows)
+    int32_t idx;      // vocab index
+};
+
+// Launch plan: how a row is split into chunks and how the workspace is laid out.
+struct Plan {
+    int32_t elems;    // elements per thread (E)
+    int32_t chunk;    // elements per chunk (kThreads * E)
+    int32_t chunks;   // chunks per row (S)
+    int32_t cand_cap; // candidate slots per chunk
+    size_t off_tickets, off_stats, off_cands, off_rows, off_ybuf, total;
+};
+
+bool make_plan(int32_t batch, int32_t vocab, int32_t dtype, int32_t max_top_k, int32_t num_logprobs,
+               Plan *plan);
+
+// Everything a kernel needs, passed by value.
+struct Args {
+    const void *logits;
+    int64_t row_stride;
+    int32_t B, V, N;
+    uint32_t options;
+    const klsample_row_params *params;
+    const int32_t *hist_ids;
+    const int32_t *hist_off;
+    int64_t *token;
+    float *logprob;
+    int32_t *top_ids;
+    float *top_lp;
+    float *probs;
+    klsample_row_info *row_info;
+    uint32_t *tickets;
+    ChunkStat *stats;
+    Cand *cands;
+    klsample_row_info *rows;
+    float *ybuf;
+    int32_t E, C, S, cand_cap;
+    int32_t vec_ok;   // 16-byte vector loads are legal for every row
+    int32_t xcd_map;  // place all chunks of a row on one XCD
+};
+
+hipError_t launch_sample(const Args &args, int32_t dtype, hipStream_t stream);
+hipError_t launch_zero_fill(void *ptr, size_t bytes, hipStream_t stream);
+
+}  // namespace kls

@@ -1,0 +1,1232 @@
+// gfx950 kernels of the fused token-sampling path.
+//
+// Per row the work is the reference's serving/sampling.py:44-63 (penalties, greedy or
+// temperature -> top-k -> top-p -> draw, log-softmax, top-N), restructured for one
+// streaming pass over the [B, V] logits:
+//
+//   scan_kernel     grid = B * S workgroups of 256 threads; workgroup (row, chunk)
+//                   loads its chunk of E elements per thread into registers with
+//                   16-byte loads, applies the penalties from an LDS count table of
+//                   the row's history, reduces max / argmax / sum-exp with wave64
+//                   shuffles, and writes the chunk's candidates: every element at or
+//                   above a lower bound on the chunk's K-th largest value, found by a
+//                   one-wave bisection over the keys of per-thread group maxima.
+//                   The last workgroup of a row to finish (atomic ticket) combines
+//                   the row.
+//   combine_row     sorts the row's candidates in LDS (bitonic, <= 2048), applies
+//                   top-k / top-p exactly on them, draws by inverse CDF in vocab
+//                   order, and writes token, logprob and top-N.  Rows the candidates
+//                   cannot settle (top-p mass beyond the candidates, slot overflow on
+//                   massive ties) are marked for dense_kernel.
+//   dense_kernel    one workgroup per row; rows not marked exit at once.  A marked
+//                   row is resolved by radix selects over the whole row (count- and
+//                   mass-weighted, 8-bit digits, LDS histograms).
+//   probs_kernel    optional: the final probability vector of each row.
+//
+// There is no dense contraction anywhere, so no MFMA: the streaming pass is bound by
+// HBM bandwidth (bytes per row = V * sizeof(logit) + 4 * H).
+
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdint.h>
+
+#include "internal.h"
+
+namespace kls {
+namespace {
+
+constexpr float kNegInf = -__builtin_huge_valf();
+constexpr double kFixScale = 1099511627776.0;  // 2^40: fixed-point unit of the row path's masses
+constexpr int kPathPending = -1;               // row state: waiting for dense_kernel
+
+__device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
+__device__ __forceinline__ int wave_id() { return threadIdx.x >> 6; }
+
+// Order-preserving 32-bit key of a float; -0.0 and +0.0 share a key because the
+// reference's comparisons treat them as equal.
+__device__ __forceinline__ uint32_t fkey(float y) {
+    uint32_t u = __float_as_uint(y);
+    if (u == 0x80000000u) u = 0u;
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+__device__ __forceinline__ float fkey_inv(uint32_t k) {
+    return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
+}
+
+// exp(d) for d <= 0 via the hardware base-2 exponential; used for sums whose
+// relative accuracy only needs to be ~1e-7.
+__device__ __forceinline__ float exp_fast(float d) {
+    return __builtin_amdgcn_exp2f(d * 1.4426950408889634f);
+}
+
+__device__ __forceinline__ int row_mode(const klsample_row_params &p, int V) {
+    if (p.flags & KLSAMPLE_ROW_GREEDY) return kGreedy;
+    if (p.top_k > 0 && p.top_k < V) return kTopK;
+    if (p.flags & KLSAMPLE_ROW_TOP_P) return kTopP;
+    return kFull;
+}
+
+// Repetition penalty (serving/sampling.py:49: s*r if s<0 else s/r, fp32, true
+// division), then presence/frequency: s - fp32(fp32(beta*count) + alpha), no FMA.
+__device__ __forceinline__ float penalize(float s, uint32_t count, const klsample_row_params &p) {
+    if (p.flags & KLSAMPLE_ROW_REPETITION)
+        s = (s < 0.f) ? __fmul_rn(s, p.repetition_penalty) : __fdiv_rn(s, p.repetition_penalty);
+    if (p.flags & KLSAMPLE_ROW_PRESENCE_FREQUENCY) {
+        float t = __fmul_rn(p.frequency_penalty, (float)count);
+        t = __fadd_rn(t, p.presence_penalty);
+        s = __fsub_rn(s, t);
+    }
+    return s;
+}
+
+__device__ __forceinline__ bool has_penalty(const Args &a, const klsample_row_params &p, int row) {
+    if (!(p.flags & (KLSAMPLE_ROW_REPETITION | KLSAMPLE_ROW_PRESENCE_FREQUENCY))) return false;
+    if (a.hist_off == nullptr) return false;
+    return a.hist_off[row + 1] > a.hist_off[row];
+}
+
+// ---------------------------------------------------------------------------------
+// LDS scratch shared by all phases of a workgroup.
+struct Misc {
+    union {
+        float f[kWaves];
+        double d[kWaves];
+        int i[kWaves];
+        uint32_t u[kWaves];
+        unsigned long long q[kWaves];
+    } red;
+    uint32_t hist[256];
+    unsigned long long hmass[256];
+    int topn_idx[kMaxLogprobs];
+    float topn_y[kMaxLogprobs];
+    uint32_t bound_key;
+    int ncand;
+    int last;
+    int flag;
+    uint32_t sel_digit;
+    uint32_t sel_need;
+    unsigned long long sel_above_mass;
+    uint32_t sel_above_count;
+    int sel_found;
+    int ia, ib;
+    double da, db;
+};
+
+template <typename T, typename Op>
+__device__ T block_reduce(T v, Op op, T *scratch) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = op(v, __shfl_xor(v, o, 64));
+    __syncthreads();
+    if (lane_id() == 0) scratch[wave_id()] = v;
+    __syncthreads();
+    T r = scratch[0];
+#pragma unroll
+    for (int w = 1; w < kWaves; ++w) r = op(r, scratch[w]);
+    return r;
+}
+
+struct OpMaxF { __device__ float operator()(float a, float b) const { return fmaxf(a, b); } };
+struct OpMinI { __device__ int operator()(int a, int b) const { return a < b ? a : b; } };
+struct OpMaxI { __device__ int operator()(int a, int b) const { return a > b ? a : b; } };
+struct OpSumI { __device__ int operator()(int a, int b) const { return a + b; } };
+struct OpSumD { __device__ double operator()(double a, double b) const { return a + b; } };
+struct OpSumQ {
+    __device__ unsigned long long operator()(unsigned long long a, unsigned long long b) const { return a + b; }
+};
+struct OpOrI { __device__ int operator()(int a, int b) const { return a | b; } };
+
+__device__ __forceinline__ float block_max(float v, Misc &ms) { return block_reduce(v, OpMaxF(), ms.red.f); }
+__device__ __forceinline__ int block_min(int v, Misc &ms) { return block_reduce(v, OpMinI(), ms.red.i); }
+__device__ __forceinline__ int block_maxi(int v, Misc &ms) { return block_reduce(v, OpMaxI(), ms.red.i); }
+__device__ __forceinline__ int block_sum(int v, Misc &ms) { return block_reduce(v, OpSumI(), ms.red.i); }
+__device__ __forceinline__ double block_sumd(double v, Misc &ms) { return block_reduce(v, OpSumD(), ms.red.d); }
+__device__ __forceinline__ unsigned long long block_sumq(unsigned long long v, Misc &ms) {
+    return block_reduce(v, OpSumQ(), ms.red.q);
+}
+
+// Exclusive scan over the workgroup in thread order; `total` receives the sum.
+template <typename T>
+__device__ T block_excl_scan(T v, T *scratch, T &total) {
+    const int lane = lane_id(), wave = wave_id();
+    T incl = v;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        T y = __shfl_up(incl, o, 64);
+        if (lane >= o) incl += y;
+    }
+    T excl = __shfl_up(incl, 1, 64);
+    if (lane == 0) excl = T(0);
+    __syncthreads();
+    if (lane == 63) scratch[wave] = incl;
+    __syncthreads();
+    T base = T(0), tot = T(0);
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+        const T s = scratch[w];
+        if (w < wave) base += s;
+        tot += s;
+    }
+    total = tot;
+    return base + excl;
+}
+
+// ---------------------------------------------------------------------------------
+// Logits loaders: 16-byte vectors of fp32 (4) or bf16 (8) elements.
+template <typename TIn> struct Loader;
+template <> struct Loader<float> {
+    static constexpr int VW = 4;
+    __device__ static __forceinline__ void vec(const float *p, float *o) {
+        const float4 v = *reinterpret_cast<const float4 *>(p);
+        o[0] = v.x; o[1] = v.y; o[2] = v.z; o[3] = v.w;
+    }
+    __device__ static __forceinline__ float one(const float *p) { return *p; }
+};
+template <> struct Loader<uint16_t> {
+    static constexpr int VW = 8;
+    __device__ static __forceinline__ float bf(uint32_t h) { return __uint_as_float(h << 16); }
+    __device__ static __forceinline__ void vec(const uint16_t *p, float *o) {
+        const uint4 v = *reinterpret_cast<const uint4 *>(p);
+        o[0] = bf(v.x & 0xffffu); o[1] = bf(v.x >> 16);
+        o[2] = bf(v.y & 0xffffu); o[3] = bf(v.y >> 16);
+        o[4] = bf(v.z & 0xffffu); o[5] = bf(v.z >> 16);
+        o[6] = bf(v.w & 0xffffu); o[7] = bf(v.w >> 16);
+    }
+    __device__ static __forceinline__ float one(const uint16_t *p) { return bf(*p); }
+};
+
+// Count table of the row's history restricted to [c0, c0 + cn): cnt[i - c0].
+template <int C>
+__device__ void build_counts(uint32_t *cnt, const Args &a, int row, int c0, int cn) {
+    uint4 *c4 = reinterpret_cast<uint4 *>(cnt);
+    for (int i = threadIdx.x; i < C / 4; i += kThreads) c4[i] = make_uint4(0u, 0u, 0u, 0u);
+    __syncthreads();
+    const int h0 = a.hist_off[row], h1 = a.hist_off[row + 1];
+    for (int h = h0 + (int)threadIdx.x; h < h1; h += kThreads) {
+        const unsigned rel = (unsigned)(a.hist_ids[h] - c0);
+        if (rel < (unsigned)cn) atomicAdd(&cnt[rel], 1u);
+    }
+    __syncthreads();
+}
+
+// Element of chunk c of `row` in final space: penalties from `cnt` (if non-null),
+// then division by T for sampled modes that stream in final space.
+template <typename TIn>
+__device__ __forceinline__ float element_final(const Args &a, const klsample_row_params &p, int row, int i,
+                                               const uint32_t *cnt, int c0, bool divide) {
+    const TIn *src = reinterpret_cast<const TIn *>(a.logits) + (int64_t)row * a.row_stride;
+    float x = Loader<TIn>::one(src + i);
+    if (cnt != nullptr) {
+        const uint32_t c = cnt[i - c0];
+        if (c) x = penalize(x, c, p);
+    }
+    if (divide) x = __fdiv_rn(x, p.temperature);
+    return x;
+}
+
+// ---------------------------------------------------------------------------------
+// Bound on the chunk's K-th largest value: the K-th largest of the maxima of
+// kThreads*G disjoint groups (E/G consecutive register elements per group).  K groups
+// have a maximum at or above it, so at least K elements are.
+template <int E, int G>
+__device__ float group_bound(const float (&x)[E], int K, uint32_t *keys, Misc &ms) {
+    constexpr int GS = E / G;
+    constexpr int NG = kThreads * G;
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        float mx = kNegInf;
+#pragma unroll
+        for (int j = 0; j < GS; ++j) mx = fmaxf(mx, x[g * GS + j]);
+        keys[g * kThreads + threadIdx.x] = fkey(mx);
+    }
+    __syncthreads();
+    if (wave_id() == 0) {
+        const int lane = lane_id();
+        uint32_t t = 0u;
+        for (int bit = 31; bit >= 0; --bit) {
+            const uint32_t cand = t | (1u << bit);
+            int c = 0;
+#pragma unroll 4
+            for (int j = lane; j < NG; j += 64) c += (keys[j] >= cand) ? 1 : 0;
+#pragma unroll
+            for (int o = 32; o > 0; o >>= 1) c += __shfl_xor(c, o, 64);
+            if (c >= K) t = cand;
+        }
+        if (lane == 0) ms.bound_key = t;
+    }
+    __syncthreads();
+    return fkey_inv(ms.bound_key);
+}
+
+template <int E>
+__device__ float chunk_bound(const float (&x)[E], int K, uint32_t *keys, Misc &ms) {
+    // smallest G with kThreads*G >= 4K (tight bound), capped by E and kMaxGroupKeys
+    int G = 1;
+    while (G < E && G * kThreads < kMaxGroupKeys && G * kThreads < 4 * K) G <<= 1;
+    if (K > G * kThreads) return kNegInf;   // fewer groups than K: no bound, keep all
+    switch (G) {
+        case 1: return group_bound<E, 1>(x, K, keys, ms);
+        case 2: if constexpr (E >= 2) return group_bound<E, 2>(x, K, keys, ms); break;
+        case 4: if constexpr (E >= 4) return group_bound<E, 4>(x, K, keys, ms); break;
+        case 8: if constexpr (E >= 8) return group_bound<E, 8>(x, K, keys, ms); break;
+        default: if constexpr (E >= 16) return group_bound<E, 16>(x, K, keys, ms); break;
+    }
+    return kNegInf;
+}
+
+// ---------------------------------------------------------------------------------
+// Radix selection over a row's entries.  A source enumerates (key, index, score)
+// for the entries it contains; each thread visits a disjoint subset.
+
+struct CandSource {
+    const Cand *cands;
+    const ChunkStat *st;
+    int S, cap;
+    float lo;
+    template <class F>
+    __device__ void each(F f) const {
+        for (int c = 0; c < S; ++c) {
+            const int n = min(st[c].ncand, cap);
+            const Cand *p = cands + (size_t)c * cap;
+            for (int j = threadIdx.x; j < n; j += kThreads) {
+                const Cand e = p[j];
+                if (e.y >= lo) f(fkey(e.y), e.idx, e.y);
+            }
+        }
+    }
+};
+
+// Dense row in final space; an entry is included when its score is above `cut`, or
+// equal to it with index <= cut_idx (cut = -inf, cut_idx = V includes everything).
+struct DenseSource {
+    const float *y;
+    int V;
+    float cut;
+    int cut_idx;
+    __device__ __forceinline__ bool keep(float v, int i) const { return v > cut || (v == cut && i <= cut_idx); }
+    template <class F>
+    __device__ void each(F f) const {
+        for (int i = threadIdx.x; i < V; i += kThreads) {
+            const float v = y[i];
+            if (keep(v, i)) f(fkey(v), i, v);
+        }
+    }
+};
+
+// Wave 0 scans 256 histogram bins from the highest digit down and records the
+// first bin at which the running count reaches `need`.
+__device__ void pick_digit_count(Misc &ms, uint32_t need) {
+    if (threadIdx.x < 64) {
+        const int l = lane_id();
+        uint32_t c[4], s = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) { c[j] = ms.hist[255 - 4 * l - j]; s += c[j]; }
+        uint32_t incl = s;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const uint32_t y = __shfl_up(incl, o, 64);
+            if (l >= o) incl += y;
+        }
+        const uint32_t excl = incl - s;
+        const unsigned long long bal = __ballot(incl >= need);
+        const int first = bal ? (__ffsll((long long)bal) - 1) : 63;
+        if (l == first) {
+            uint32_t acc = excl;
+            int digit = 255 - 4 * l - 3;
+            uint32_t rem = need > acc ? need - acc : 1u;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                if (acc + c[j] >= need) { digit = 255 - 4 * l - j; rem = need - acc; break; }
+                acc += c[j];
+            }
+            ms.sel_digit = (uint32_t)digit;
+            ms.sel_need = rem;
+        }
+    }
+    __syncthreads();
+}
+
+// Key of the R-th largest entry of `src` (R >= 1, R <= number of entries).
+template <typename Src>
+__device__ uint32_t select_kth(const Src &src, uint32_t R, Misc &ms) {
+    uint32_t prefix = 0u, need = R;
+    for (int shift = 24; shift >= 0; shift -= 8) {
+        const uint32_t hmask = (shift == 24) ? 0u : (0xffffffffu << (shift + 8));
+        for (int i = threadIdx.x; i < 256; i += kThreads) ms.hist[i] = 0u;
+        __syncthreads();
+        src.each([&](uint32_t key, int, float) {
+            if ((key & hmask) == prefix) atomicAdd(&ms.hist[(key >> shift) & 255u], 1u);
+        });
+        __syncthreads();
+        pick_digit_count(ms, need);
+        prefix |= ms.sel_digit << shift;
+        need = ms.sel_need;
+        __syncthreads();
+    }
+    return prefix;
+}
+
+// Mass-weighted selection: walking entries from the largest score down in groups of
+// equal score, find the first group g whose cumulative fixed-point mass (all groups
+// above g plus g itself) exceeds `target`.  Returns false if the total does not.
+struct MassPick {
+    uint32_t key;                  // key of group g
+    unsigned long long above;      // mass of all entries above g
+    uint32_t above_count;          // entries above g
+    uint32_t group_count;          // entries in g
+    unsigned long long group_mass; // mass of g
+};
+
+template <typename Src>
+__device__ bool select_mass(const Src &src, double target, double m, MassPick &out, Misc &ms) {
+    uint32_t prefix = 0u;
+    unsigned long long above = 0ull;
+    uint32_t above_count = 0u;
+    for (int shift = 24; shift >= 0; shift -= 8) {
+        const uint32_t hmask = (shift == 24) ? 0u : (0xffffffffu << (shift + 8));
+        for (int i = threadIdx.x; i < 256; i += kThreads) { ms.hist[i] = 0u; ms.hmass[i] = 0ull; }
+        __syncthreads();
+        src.each([&](uint32_t key, int, float v) {
+            if ((key & hmask) == prefix) {
+                const uint32_t b = (key >> shift) & 255u;
+                const double w = exp((double)v - m);
+                atomicAdd(&ms.hist[b], 1u);
+                atomicAdd(&ms.hmass[b], (unsigned long long)__double2ull_rn(w * kFixScale));
+            }
+        });
+        __syncthreads();
+        if (threadIdx.x < 64) {
+            const int l = lane_id();
+            unsigned long long c[4], s = 0ull;
+            uint32_t n[4], ns = 0u;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                c[j] = ms.hmass[255 - 4 * l - j]; s += c[j];
+                n[j] = ms.hist[255 - 4 * l - j]; ns += n[j];
+            }
+            unsigned long long incl = s;
+            uint32_t nincl = ns;
+#pragma unroll
+            for (int o = 1; o < 64; o <<= 1) {
+                const unsigned long long y = __shfl_up(incl, o, 64);
+                const uint32_t ny = __shfl_up(nincl, o, 64);
+                if (l >= o) { incl += y; nincl += ny; }
+            }
+            const unsigned long long bal = __ballot((double)(above + incl) > target);
+            if (bal == 0ull) {
+                if (l == 0) ms.sel_found = 0;
+            } else if (l == __ffsll((long long)bal) - 1) {
+                unsigned long long acc = above + (incl - s);
+                uint32_t nacc = above_count + (nincl - ns);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    if ((double)(acc + c[j]) > target) {
+                        ms.sel_digit = (uint32_t)(255 - 4 * l - j);
+                        ms.sel_above_mass = acc;
+                        ms.sel_above_count = nacc;
+                        ms.sel_need = n[j];
+                        ms.hmass[0] = c[j];  // group mass at the final level (read below)
+                        break;
+                    }
+                    acc += c[j];
+                    nacc += n[j];
+                }
+                ms.sel_found = 1;
+            }
+        }
+        __syncthreads();
+        if (!ms.sel_found) { __syncthreads(); return false; }
+        prefix |= ms.sel_digit << shift;
+        above = ms.sel_above_mass;
+        above_count = ms.sel_above_count;
+        out.group_count = ms.sel_need;
+        out.group_mass = ms.hmass[0];
+        __syncthreads();
+    }
+    out.key = prefix;
+    out.above = above;
+    out.above_count = above_count;
+    return true;
+}
+
+// Walk items [0, n) in order; `weight(i)` >= 0.  Returns the first item whose
+// inclusive cumulative weight exceeds `target`, or -1; `last` receives the last item
+// with positive weight (-1 if none).
+template <typename W>
+__device__ int ordered_find(int n, W weight, double target, Misc &ms, int &last, double &before) {
+    double base = 0.0;
+    int lastp = -1;
+    for (int t0 = 0; t0 < n; t0 += kThreads * 4) {
+        const int i0 = t0 + 4 * (int)threadIdx.x;
+        double w[4], s = 0.0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) { w[j] = (i0 + j < n) ? weight(i0 + j) : 0.0; s += w[j]; }
+        double tot;
+        const double ex = block_excl_scan(s, ms.red.d, tot);
+        double c = base + ex;
+        int loc = 0x7fffffff, lp = -1;
+        double cb = 0.0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            if (w[j] > 0.0) {
+                if (loc == 0x7fffffff && c + w[j] > target) { loc = i0 + j; cb = c; }
+                c += w[j];
+                lp = i0 + j;
+            }
+        }
+        const int found = block_min(loc, ms);
+        lp = block_maxi(lp, ms);
+        if (lp >= 0) lastp = lp;
+        if (found != 0x7fffffff) {
+            if (loc == found) ms.da = cb;
+            __syncthreads();
+            before = ms.da;
+            last = lastp;
+            __syncthreads();
+            return found;
+        }
+        base += tot;
+    }
+    last = lastp;
+    before = base;
+    return -1;
+}
+
+// Bitonic sort (ascending) of n = power of two 64-bit keys in LDS.
+__device__ void bitonic_sort(unsigned long long *s, int n) {
+    for (int k = 2; k <= n; k <<= 1) {
+        for (int j = k >> 1; j > 0; j >>= 1) {
+            for (int i = threadIdx.x; i < n; i += kThreads) {
+                const int l = i ^ j;
+                if (l > i) {
+                    const unsigned long long x = s[i], y = s[l];
+                    const bool up = (i & k) == 0;
+                    if ((x > y) == up) { s[i] = y; s[l] = x; }
+                }
+            }
+            __syncthreads();
+        }
+    }
+}
+
+__device__ __forceinline__ int pow2_ceil(int n) {
+    int p = 1;
+    while (p < n) p <<= 1;
+    return p;
+}
+
+// Sort key: ascending order = score descending, then index ascending.
+__device__ __forceinline__ unsigned long long desc_key(float y, int idx) {
+    return ((unsigned long long)(~fkey(y)) << 32) | (uint32_t)idx;
+}
+__device__ __forceinline__ float desc_key_y(unsigned long long k) { return fkey_inv(~(uint32_t)(k >> 32)); }
+__device__ __forceinline__ int desc_key_idx(unsigned long long k) { return (int)(uint32_t)k; }
+
+
+// ---------------------------------------------------------------------------------
+// Outputs of a resolved row.
+
+struct RowOut {
+    int token;
+    double logprob;
+    float m;          // max final score
+    float cut;        // smallest kept score
+    int cut_idx;      // largest kept index among scores equal to `cut`
+    int kept;
+    double log_norm;  // log of the kept mass relative to exp(m)
+    int path;
+};
+
+// Thread 0 writes token / logprob / row state; all threads write the top-N list
+// from ms.topn_* (`count` finite entries, best first).  Slots from `count` up to
+// min(N, V) are -inf entries whose ids are the smallest not already listed;
+// slots beyond min(N, V) (only when V < N) hold id -1.
+__device__ void write_row(const Args &a, int row, int mode, const RowOut &r, int count, Misc &ms) {
+    const int N = a.N, V = a.V;
+    if (N > 0) {
+        const int nv = min(N, V);
+        int32_t *ids = a.top_ids + (size_t)row * N;
+        float *lps = a.top_lp + (size_t)row * N;
+        for (int t = threadIdx.x; t < N; t += kThreads) {
+            if (t < count && t < nv) {
+                ids[t] = ms.topn_idx[t];
+                lps[t] = (float)((double)ms.topn_y[t] - (double)r.m - r.log_norm);
+            } else if (t >= nv) {
+                ids[t] = -1;
+                lps[t] = kNegInf;
+            }
+        }
+        if (count < nv) {
+            // the answer lies in [0, count + nv) <= [0, 2N): a bitmap of listed ids
+            uint32_t *bm = ms.hist;
+            __syncthreads();
+            for (int i = threadIdx.x; i < 256; i += kThreads) bm[i] = 0u;
+            __syncthreads();
+            for (int t = threadIdx.x; t < count; t += kThreads) {
+                const int id = ms.topn_idx[t];
+                if (id < 2 * kMaxLogprobs) atomicOr(&bm[id >> 5], 1u << (id & 31));
+            }
+            __syncthreads();
+            if (threadIdx.x == 0) {
+                int j = 0;
+                for (int t = count; t < nv; ++t) {
+                    while ((bm[j >> 5] >> (j & 31)) & 1u) ++j;
+                    ids[t] = j;
+                    lps[t] = kNegInf;
+                    ++j;
+                }
+            }
+        }
+    }
+    if (threadIdx.x == 0) {
+        a.token[row] = r.token;
+        a.logprob[row] = (float)r.logprob;
+        klsample_row_info info;
+        info.max_score = r.m;
+        info.cut_score = r.cut;
+        info.cut_index = r.cut_idx;
+        info.kept = r.kept;
+        info.log_norm = r.log_norm;
+        info.path = r.path;
+        info.mode = mode;
+        a.rows[row] = info;
+        if (a.row_info) a.row_info[row] = info;
+    }
+}
+
+// Top-N of the entries of a dense source, best first, into ms.topn_*; ties at the
+// N-th score are taken in index order.  Returns the number written.
+__device__ int dense_topn(const DenseSource &src, int N, unsigned long long *sortbuf, Misc &ms) {
+    if (N <= 0) return 0;
+    int total = 0;
+    src.each([&](uint32_t, int, float) { ++total; });
+    total = block_sum(total, ms);
+    const int want = min(N, total);
+    if (want == 0) return 0;
+    const uint32_t kN = select_kth(src, (uint32_t)want, ms);
+    if (threadIdx.x == 0) ms.ncand = 0;
+    __syncthreads();
+    src.each([&](uint32_t key, int idx, float y) {
+        if (key > kN) {
+            const int pos = atomicAdd(&ms.ncand, 1);
+            ms.topn_idx[pos] = idx;
+            ms.topn_y[pos] = y;
+        }
+    });
+    __syncthreads();
+    const int ngt = ms.ncand;
+    const int need = want - ngt;
+    const float tauN = fkey_inv(kN);
+    int base = 0;
+    for (int t0 = 0; t0 < src.V && base < need; t0 += kThreads * 4) {
+        const int i0 = t0 + 4 * (int)threadIdx.x;
+        int f[4], s = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int i = i0 + j;
+            f[j] = 0;
+            if (i < src.V) {
+                const float v = src.y[i];
+                f[j] = (fkey(v) == kN && src.keep(v, i)) ? 1 : 0;
+            }
+            s += f[j];
+        }
+        int tot;
+        int rank = base + block_excl_scan(s, ms.red.i, tot);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            if (f[j]) {
+                if (rank < need) { ms.topn_idx[ngt + rank] = i0 + j; ms.topn_y[ngt + rank] = tauN; }
+                ++rank;
+            }
+        }
+        base += tot;
+    }
+    __syncthreads();
+    const int n2 = pow2_ceil(want);
+    for (int i = threadIdx.x; i < n2; i += kThreads)
+        sortbuf[i] = (i < want) ? desc_key(ms.topn_y[i], ms.topn_idx[i]) : ~0ull;
+    __syncthreads();
+    bitonic_sort(sortbuf, n2);
+    for (int i = threadIdx.x; i < want; i += kThreads) {
+        ms.topn_idx[i] = desc_key_idx(sortbuf[i]);
+        ms.topn_y[i] = desc_key_y(sortbuf[i]);
+    }
+    __syncthreads();
+    return want;
+}
+
+// Multi-pass row path: materialise the row's final scores in the workspace, then
+// resolve top-k / top-p / the draw / top-N with radix selects over the whole row.
+// Taken when the chunk candidates cannot settle the row.
+template <typename TIn, int E>
+__device__ void dense_resolve(const Args &a, int row, const klsample_row_params &p, int mode,
+                              unsigned char *raw, Misc &ms) {
+    constexpr int C = kThreads * E;
+    const int V = a.V;
+    float *yb = a.ybuf + (size_t)row * V;
+    const bool pen = has_penalty(a, p, row);
+    uint32_t *cnt = reinterpret_cast<uint32_t *>(raw);
+    float mt = kNegInf;
+    int at = 0x7fffffff;
+    for (int c = 0; c < a.S; ++c) {
+        const int c0 = c * C, cn = min(C, V - c0);
+        if (pen) build_counts<C>(cnt, a, row, c0, cn);
+        for (int i = threadIdx.x; i < cn; i += kThreads) {
+            const float y = element_final<TIn>(a, p, row, c0 + i, pen ? cnt : nullptr, c0, mode != kGreedy);
+            yb[c0 + i] = y;
+            if (y > mt) { mt = y; at = c0 + i; }
+        }
+        __syncthreads();
+    }
+    const float m = block_max(mt, ms);
+    int arg = block_min(mt == m ? at : 0x7fffffff, ms);
+    if (arg == 0x7fffffff) arg = 0;
+    __syncthreads();
+    const double md = (double)m;
+    auto wfix = [md](float y) -> unsigned long long {
+        return (unsigned long long)__double2ull_rn(exp((double)y - md) * kFixScale);
+    };
+    unsigned long long *sortbuf = reinterpret_cast<unsigned long long *>(raw);
+    RowOut r;
+    r.m = m;
+    r.path = 1;
+    const DenseSource all{yb, V, kNegInf, V};
+    int count = 0;
+    if (mode == kGreedy) {
+        unsigned long long zq = 0ull;
+        all.each([&](uint32_t, int, float y) { zq += wfix(y); });
+        zq = block_sumq(zq, ms);
+        r.token = arg;
+        r.log_norm = log((double)zq / kFixScale);
+        r.logprob = -r.log_norm;
+        r.cut = kNegInf;
+        r.cut_idx = V;
+        r.kept = V;
+        count = dense_topn(all, a.N, sortbuf, ms);
+    } else {
+        float lo = kNegInf;
+        if (mode == kTopK) lo = fkey_inv(select_kth(all, (uint32_t)p.top_k, ms));
+        const DenseSource ge{yb, V, lo, V};
+        unsigned long long zk = 0ull;
+        int nk = 0;
+        ge.each([&](uint32_t, int, float y) { zk += wfix(y); ++nk; });
+        zk = block_sumq(zk, ms);
+        nk = block_sum(nk, ms);
+        float cut = lo;
+        int cut_idx = V, kept = nk;
+        unsigned long long zf = zk;
+        if (p.flags & KLSAMPLE_ROW_TOP_P) {
+            const double target = (double)p.top_p * (double)zk;
+            MassPick mp;
+            if (select_mass(ge, target, md, mp, ms)) {
+                const unsigned long long wt = mp.group_count ? mp.group_mass / mp.group_count : 0ull;
+                uint32_t keep = mp.group_count;
+                if (wt > 0ull) {
+                    const double room = target - (double)mp.above;
+                    const double k = floor(room / (double)wt) + 1.0;
+                    keep = (uint32_t)fmin((double)mp.group_count, fmax(1.0, k));
+                }
+                cut = fkey_inv(mp.key);
+                kept = (int)(mp.above_count + keep);
+                zf = mp.above + (unsigned long long)keep * wt;
+                if (keep < mp.group_count) {
+                    const float tie = cut;
+                    int lastt;
+                    double bt;
+                    cut_idx = ordered_find(
+                        V, [&](int i) { return yb[i] == tie ? 1.0 : 0.0; }, (double)keep - 0.5, ms, lastt, bt);
+                    if (cut_idx < 0) cut_idx = V;
+                }
+            }
+        }
+        const DenseSource ks{yb, V, cut, cut_idx};
+        int last;
+        double before;
+        int tok = ordered_find(
+            V, [&](int i) { const float y = yb[i]; return ks.keep(y, i) ? (double)wfix(y) : 0.0; },
+            (double)p.uniform * (double)zf, ms, last, before);
+        if (tok < 0) tok = last >= 0 ? last : 0;
+        r.token = tok;
+        r.cut = cut;
+        r.cut_idx = cut_idx;
+        r.kept = kept;
+        r.log_norm = log((double)zf / kFixScale);
+        r.logprob = (double)yb[tok] - md - r.log_norm;
+        count = dense_topn(ks, a.N, sortbuf, ms);
+    }
+    write_row(a, row, mode, r, count, ms);
+}
+
+// Resolve one row from its chunk summaries and candidates (or hand it to
+// dense_resolve).  Runs in one workgroup of kThreads.
+// Resolve one row from its chunk summaries and candidates.  Runs in one workgroup
+// of kThreads.  Returns false when the candidates cannot settle the row; the row is
+// then marked for dense_kernel.
+template <typename TIn, int E>
+__device__ bool combine_row(const Args &a, int row, const klsample_row_params &p, int mode,
+                            unsigned char *raw, Misc &ms) {
+    constexpr int C = kThreads * E;
+    const int S = a.S, V = a.V, N = a.N;
+    const ChunkStat *st = a.stats + (size_t)row * S;
+    const Cand *cands = a.cands + (size_t)row * S * a.cand_cap;
+
+    float m = kNegInf, lo = kNegInf;
+    int ovf = 0;
+    for (int c = threadIdx.x; c < S; c += kThreads) {
+        const ChunkStat s = st[c];
+        m = fmaxf(m, s.m);
+        lo = fmaxf(lo, s.y_thr);
+        ovf |= s.overflow;
+    }
+    m = block_max(m, ms);
+    lo = block_max(lo, ms);
+    ovf = block_reduce(ovf, OpOrI(), ms.red.i);
+    if (ovf || (a.options & KLSAMPLE_OPT_FORCE_DENSE)) { return false; }
+    int arg = 0x7fffffff;
+    double Z = 0.0;
+    for (int c = threadIdx.x; c < S; c += kThreads) {
+        const ChunkStat s = st[c];
+        if (mode == kGreedy && s.m == m) arg = min(arg, s.arg);
+        if (s.m > kNegInf) Z += s.z * exp((double)s.m - (double)m);
+    }
+    arg = block_min(arg, ms);
+    Z = block_sumd(Z, ms);
+
+    // candidate set F = { y >= lo }: complete above lo
+    CandSource src{cands, st, S, a.cand_cap, lo};
+    int nF = 0;
+    src.each([&](uint32_t, int, float) { ++nF; });
+    nF = block_sum(nF, ms);
+    const int R = (mode == kTopK) ? p.top_k : (mode == kTopP ? kSortCap / 2 : N);
+    if (nF > kSortCap) {
+        if (R < 1 || R > kSortCap || R > nF) { return false; }
+        src.lo = fkey_inv(select_kth(src, (uint32_t)R, ms));
+        nF = 0;
+        src.each([&](uint32_t, int, float) { ++nF; });
+        nF = block_sum(nF, ms);
+        if (nF > kSortCap) { return false; }
+    }
+    unsigned long long *sb = reinterpret_cast<unsigned long long *>(raw);
+    if (threadIdx.x == 0) ms.ncand = 0;
+    __syncthreads();
+    src.each([&](uint32_t, int idx, float y) {
+        const int pos = atomicAdd(&ms.ncand, 1);
+        sb[pos] = desc_key(y, idx);
+    });
+    __syncthreads();
+    const int n2 = pow2_ceil(nF > 0 ? nF : 1);
+    for (int i = nF + (int)threadIdx.x; i < n2; i += kThreads) sb[i] = ~0ull;
+    __syncthreads();
+    bitonic_sort(sb, n2);
+
+    RowOut r;
+    r.path = 0;
+    int count = 0;
+    if (mode == kGreedy || mode == kFull) {
+        count = min(N, nF);
+        for (int t = threadIdx.x; t < count; t += kThreads) {
+            ms.topn_idx[t] = desc_key_idx(sb[t]);
+            ms.topn_y[t] = desc_key_y(sb[t]);
+        }
+        __syncthreads();
+        r.m = m;
+        r.cut = kNegInf;
+        r.cut_idx = V;
+        r.kept = V;
+        r.log_norm = log(Z);
+        if (mode == kGreedy) {
+            r.token = (arg == 0x7fffffff) ? 0 : arg;
+            r.logprob = -r.log_norm;
+        } else {
+            // chunk-level inverse CDF, then an ordered rescan of the chosen chunk
+            const double target = (double)p.uniform * Z;
+            int lastc;
+            double before;
+            int c = ordered_find(
+                S, [&](int i) { const ChunkStat s = st[i]; return s.m > kNegInf ? s.z * exp((double)s.m - (double)m) : 0.0; },
+                target, ms, lastc, before);
+            if (c < 0) { c = lastc >= 0 ? lastc : 0; }
+            const ChunkStat sc = st[c];
+            const int c0 = c * C, cn = min(C, V - c0);
+            const bool pen = has_penalty(a, p, row);
+            uint32_t *cnt = reinterpret_cast<uint32_t *>(raw);
+            if (pen) build_counts<C>(cnt, a, row, c0, cn);
+            const double scale = exp((double)sc.m - (double)m);
+            const double rem = (target - before) / scale;
+            int lastj;
+            double bj;
+            int j = ordered_find(
+                cn, [&](int i) {
+                    const float y = element_final<TIn>(a, p, row, c0 + i, pen ? cnt : nullptr, c0, true);
+                    return (double)exp_fast(y - sc.m);
+                },
+                rem, ms, lastj, bj);
+            if (j < 0) j = lastj >= 0 ? lastj : 0;
+            r.token = c0 + j;
+            const float yt = element_final<TIn>(a, p, row, r.token, pen ? cnt : nullptr, c0, true);
+            r.logprob = (double)yt - (double)m - r.log_norm;
+            __syncthreads();
+        }
+        write_row(a, row, mode, r, count, ms);
+        return true;
+    }
+
+    // top-k (optionally followed by top-p) or top-p alone, over the sorted candidates
+    int L0;
+    double mref;
+    if (mode == kTopK) {
+        const int kk = p.top_k;
+        const float tau = (nF >= kk) ? desc_key_y(sb[kk - 1]) : kNegInf;
+        int c = 0;
+        for (int i = threadIdx.x; i < nF; i += kThreads) c += (desc_key_y(sb[i]) >= tau) ? 1 : 0;
+        L0 = block_sum(c, ms);
+        mref = nF > 0 ? (double)desc_key_y(sb[0]) : 0.0;
+    } else {
+        L0 = nF;
+        mref = (double)m;
+    }
+    if (L0 == 0) {
+        // every score is -inf: nothing can be drawn
+        r.m = m; r.cut = kNegInf; r.cut_idx = V; r.kept = 0; r.log_norm = 0.0;
+        r.token = 0; r.logprob = __builtin_nan("");
+        write_row(a, row, mode, r, 0, ms);
+        return true;
+    }
+    const int seg = (L0 + kThreads - 1) / kThreads;
+    const int i0 = min((int)threadIdx.x * seg, L0), i1 = min(i0 + seg, L0);
+    double s = 0.0;
+    for (int i = i0; i < i1; ++i) s += exp((double)desc_key_y(sb[i]) - mref);
+    double tot;
+    const double ex = block_excl_scan(s, ms.red.d, tot);
+    const double zref = (mode == kTopK) ? tot : Z;
+    int L = L0;
+    if (p.flags & KLSAMPLE_ROW_TOP_P) {
+        const double target = (double)p.top_p * zref;
+        int cut = 0x7fffffff;
+        double c = ex;
+        for (int i = i0; i < i1; ++i) {
+            if (cut == 0x7fffffff && c > target) cut = i;
+            c += exp((double)desc_key_y(sb[i]) - mref);
+        }
+        cut = block_min(cut, ms);
+        if (cut != 0x7fffffff) {
+            L = cut;
+        } else if (mode == kTopP && lo > kNegInf) {
+            // the kept mass reaches past the complete candidate region
+            return false;
+        }
+    }
+    double zs = 0.0;
+    for (int i = i0; i < min(i1, L); ++i) zs += exp((double)desc_key_y(sb[i]) - mref);
+    const double zf = block_sumd(zs, ms);
+    const float cut_y = desc_key_y(sb[L - 1]);
+    const bool partial = (L < nF) && (desc_key_y(sb[L]) == cut_y);
+    r.m = (float)mref;
+    r.cut = cut_y;
+    r.cut_idx = partial ? desc_key_idx(sb[L - 1]) : V;
+    r.kept = L;
+    r.log_norm = log(zf);
+    count = min(N, L);
+    for (int t = threadIdx.x; t < count; t += kThreads) {
+        ms.topn_idx[t] = desc_key_idx(sb[t]);
+        ms.topn_y[t] = desc_key_y(sb[t]);
+    }
+    __syncthreads();
+    // inverse CDF over the kept set in vocab order
+    for (int i = threadIdx.x; i < L; i += kThreads) {
+        const unsigned long long k = sb[i];
+        sb[i] = ((unsigned long long)(uint32_t)desc_key_idx(k) << 32) | __float_as_uint(desc_key_y(k));
+    }
+    const int l2 = pow2_ceil(L);
+    for (int i = L + (int)threadIdx.x; i < l2; i += kThreads) sb[i] = ~0ull;
+    __syncthreads();
+    bitonic_sort(sb, l2);
+    int last;
+    double before;
+    int j = ordered_find(
+        L, [&](int i) { return exp((double)__uint_as_float((uint32_t)sb[i]) - mref); },
+        (double)p.uniform * zf, ms, last, before);
+    if (j < 0) j = last >= 0 ? last : 0;
+    r.token = (int)(sb[j] >> 32);
+    r.logprob = (double)__uint_as_float((uint32_t)sb[j]) - mref - r.log_norm;
+    __syncthreads();
+    write_row(a, row, mode, r, count, ms);
+    return true;
+}
+
+__device__ __forceinline__ void map_block(const Args &a, int &row, int &chunk) {
+    const int w = blockIdx.x;
+    if (a.xcd_map) {
+        // consecutive workgroup ids go to consecutive XCDs: keep a row's chunks on one
+        // XCD so the row's history and candidates stay in one L2
+        const int xcd = w & 7, slot = w >> 3;
+        row = xcd + 8 * (slot / a.S);
+        chunk = slot % a.S;
+    } else {
+        row = w / a.S;
+        chunk = w % a.S;
+    }
+}
+
+template <int C>
+struct RawBytes {
+    static constexpr int a = C * 4;
+    static constexpr int b = kSortCap * 8;
+    static constexpr int c = kMaxGroupKeys * 4;
+    static constexpr int ab = a > b ? a : b;
+    static constexpr int value = ab > c ? ab : c;
+};
+
+// Streaming pass: one workgroup per (row, chunk).
+template <typename TIn, int E>
+__global__ __launch_bounds__(kThreads) void scan_kernel(Args a) {
+    constexpr int VW = Loader<TIn>::VW;
+    constexpr int NV = E / VW;
+    constexpr int C = kThreads * E;
+    __shared__ __attribute__((aligned(16))) unsigned char raw[RawBytes<C>::value];
+    __shared__ Misc ms;
+
+    int row, chunk;
+    map_block(a, row, chunk);
+    const klsample_row_params p = a.params[row];
+    const int V = a.V;
+    const int tid = threadIdx.x;
+    const int mode = row_mode(p, V);
+    const int c0 = chunk * C;
+    const int cn = min(C, V - c0);
+    const TIn *src = reinterpret_cast<const TIn *>(a.logits) + (int64_t)row * a.row_stride + c0;
+    if (tid == 0) ms.ncand = 0;
+
+    float x[E];
+#pragma unroll
+    for (int v = 0; v < NV; ++v) {
+        const int li = (v * kThreads + tid) * VW;
+        if (a.vec_ok && li + VW <= cn) {
+            Loader<TIn>::vec(src + li, &x[v * VW]);
+        } else {
+#pragma unroll
+            for (int e = 0; e < VW; ++e) x[v * VW + e] = (li + e < cn) ? Loader<TIn>::one(src + li + e) : kNegInf;
+        }
+    }
+
+    if (has_penalty(a, p, row)) {
+        uint32_t *cnt = reinterpret_cast<uint32_t *>(raw);
+        build_counts<C>(cnt, a, row, c0, cn);
+#pragma unroll
+        for (int v = 0; v < NV; ++v) {
+            const int li = (v * kThreads + tid) * VW;
+#pragma unroll
+            for (int e = 0; e < VW; ++e) {
+                const uint32_t c = cnt[li + e];
+                if (c) x[v * VW + e] = penalize(x[v * VW + e], c, p);
+            }
+        }
+        __syncthreads();
+    }
+    if (mode == kTopP || mode == kFull) {
+#pragma unroll
+        for (int e = 0; e < E; ++e) x[e] = __fdiv_rn(x[e], p.temperature);
+    }
+
+    ChunkStat st;
+    st.m = kNegInf;
+    st.arg = 0x7fffffff;
+    st.y_thr = kNegInf;
+    st.ncand = 0;
+    st.z = 0.0;
+    st.overflow = 0;
+    st.pad = 0;
+    if (mode != kTopK) {
+        float mt = kNegInf;
+#pragma unroll
+        for (int e = 0; e < E; ++e) mt = fmaxf(mt, x[e]);
+        const float m = block_max(mt, ms);
+        if (mode == kGreedy) {
+            int at = 0x7fffffff;
+#pragma unroll
+            for (int v = 0; v < NV; ++v) {
+                const int li = (v * kThreads + tid) * VW;
+#pragma unroll
+                for (int e = 0; e < VW; ++e)
+                    if (x[v * VW + e] == m && li + e < cn && li + e < at) at = li + e;
+            }
+            at = block_min(at, ms);
+            st.arg = (at == 0x7fffffff) ? 0x7fffffff : c0 + at;
+        }
+        double z = 0.0;
+        if (m > kNegInf) {
+#pragma unroll
+            for (int e = 0; e < E; ++e) z += (double)exp_fast(x[e] - m);
+        }
+        st.z = block_sumd(z, ms);
+        st.m = m;
+    }
+
+    const int K = (mode == kGreedy || mode == kFull) ? a.N
+                  : (mode == kTopK ? p.top_k : max(kTopPCandidates, a.N));
+    if (K > 0) {
+        float bound = kNegInf;
+        if (K < cn) bound = chunk_bound<E>(x, K, reinterpret_cast<uint32_t *>(raw), ms);
+        else __syncthreads();
+        float thr = bound;
+        if (mode == kTopK && bound > kNegInf) {
+            // widen by 8 ulps so every element whose quotient by T rounds to at least
+            // bound / T is kept
+            const float d = fmaxf(fabsf(bound) * 9.5367431640625e-07f, p.temperature * 7.174648137343064e-43f);
+            thr = bound - d;
+        }
+        st.y_thr = (mode == kTopK) ? (bound > kNegInf ? __fdiv_rn(bound, p.temperature) : kNegInf) : bound;
+        int my = 0;
+#pragma unroll
+        for (int e = 0; e < E; ++e) my += (x[e] >= thr && x[e] > kNegInf) ? 1 : 0;
+        int incl = my;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const int y = __shfl_up(incl, o, 64);
+            if (lane_id() >= o) incl += y;
+        }
+        const int wtot = __shfl(incl, 63, 64);
+        int wbase = 0;
+        if (lane_id() == 63 && wtot > 0) wbase = atomicAdd(&ms.ncand, wtot);
+        wbase = __shfl(wbase, 63, 64);
+        int pos = wbase + incl - my;
+        Cand *out = a.cands + ((size_t)row * a.S + chunk) * a.cand_cap;
+#pragma unroll
+        for (int v = 0; v < NV; ++v) {
+            const int li = (v * kThreads + tid) * VW;
+#pragma unroll
+            for (int e = 0; e < VW; ++e) {
+                const float xv = x[v * VW + e];
+                if (xv >= thr && xv > kNegInf) {
+                    if (pos < a.cand_cap) {
+                        Cand cd;
+                        cd.y = (mode == kTopK) ? __fdiv_rn(xv, p.temperature) : xv;
+                        cd.idx = c0 + li + e;
+                        out[pos] = cd;
+                    }
+                    ++pos;
+                }
+            }
+        }
+        __syncthreads();
+        const int total = ms.ncand;
+        st.ncand = min(total, a.cand_cap);
+        st.overflow = total > a.cand_cap ? 1 : 0;
+    }
+    if (tid == 0) a.stats[(size_t)row * a.S + chunk] = st;
+    if (a.options & KLSAMPLE_OPT_SPLIT_COMBINE) return;
+
+    // the last workgroup of the row to finish combines it
+    __syncthreads();
+    if (tid == 0) {
+        __threadfence();
+        const uint32_t t = atomicAdd(&a.tickets[row], 1u);
+        ms.last = (t == (uint32_t)a.S - 1u) ? 1 : 0;
+    }
+    __syncthreads();
+    if (!ms.last) return;
+    __threadfence();
+    if (tid == 0) a.tickets[row] = 0u;
+    if (!combine_row<TIn, E>(a, row, p, mode, raw, ms) && tid == 0) a.rows[row].path = kPathPending;
+}
+
+template <typename TIn, int E>
+__global__ __launch_bounds__(kThreads) void combine_kernel(Args a) {
+    constexpr int C = kThreads * E;
+    __shared__ __attribute__((aligned(16))) unsigned char raw[RawBytes<C>::value];
+    __shared__ Misc ms;
+    const int row = blockIdx.x;
+    const klsample_row_params p = a.params[row];
+    if (!combine_row<TIn, E>(a, row, p, row_mode(p, a.V), raw, ms) && threadIdx.x == 0)
+        a.rows[row].path = kPathPending;
+}
+
+// Multi-pass path for the rows combine_row marked; every other workgroup exits at once.
+template <typename TIn, int E>
+__global__ __launch_bounds__(kThreads) void dense_kernel(Args a) {
+    constexpr int C = kThreads * E;
+    __shared__ __attribute__((aligned(16))) unsigned char raw[RawBytes<C>::value];
+    __shared__ Misc ms;
+    const int row = blockIdx.x;
+    if (a.rows[row].path != kPathPending) return;
+    const klsample_row_params p = a.params[row];
+    dense_resolve<TIn, E>(a, row, p, row_mode(p, a.V), raw, ms);
+}
+
+// Final probabilities: exp(s - max - log_norm) on the kept set, 0 elsewhere.
+template <typename TIn, int E>
+__global__ __launch_bounds__(kThreads) void probs_kernel(Args a) {
+    constexpr int C = kThreads * E;
+    __shared__ __attribute__((aligned(16))) uint32_t cnt[C];
+    int row, chunk;
+    map_block(a, row, chunk);
+    const klsample_row_params p = a.params[row];
+    const int mode = row_mode(p, a.V);
+    const klsample_row_info ri = a.rows[row];
+    const int c0 = chunk * C, cn = min(C, a.V - c0);
+    const bool pen = has_penalty(a, p, row);
+    if (pen) build_counts<C>(cnt, a, row, c0, cn);
+    for (int i = threadIdx.x; i < cn; i += kThreads) {
+        const int gi = c0 + i;
+        const float y = element_final<TIn>(a, p, row, gi, pen ? cnt : nullptr, c0, mode != kGreedy);
+        const bool kept = (mode == kGreedy || mode == kFull) ||
+                          y > ri.cut_score || (y == ri.cut_score && gi <= ri.cut_index);
+        const float pr = kept ? (float)exp((double)y - (double)ri.max_score - ri.log_norm) : 0.f;
+        a.probs[(size_t)row * a.V + gi] = pr;
+    }
+}
+
+__global__ void zero_fill_kernel(uint4 *p, size_t n16, unsigned char *tail, size_t ntail) {
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n16; i += stride)
+        p[i] = make_uint4(0u, 0u, 0u, 0u);
+    if (blockIdx.x == 0)
+        for (size_t i = threadIdx.x; i < ntail; i += blockDim.x) tail[i] = 0;
+}
+
+template <typename TIn, int E>
+hipError_t launch_typed(const Args &a, hipStream_t s) {
+    const dim3 grid((unsigned)((int64_t)a.B * a.S));
+    scan_kernel<TIn, E><<<grid, kThreads, 0, s>>>(a);
+    if (a.options & KLSAMPLE_OPT_SPLIT_COMBINE) combine_kernel<TIn, E><<<dim3((unsigned)a.B), kThreads, 0, s>>>(a);
+    dense_kernel<TIn, E><<<dim3((unsigned)a.B), kThreads, 0, s>>>(a);
+    if (a.probs) probs_kernel<TIn, E><<<grid, kThreads, 0, s>>>(a);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_sample(const Args &a, int32_t dtype, hipStream_t s) {
+    if (dtype == KLSAMPLE_FLOAT32) {
+        switch (a.E) {
+            case 4: return launch_typed<float, 4>(a, s);
+            case 8: return launch_typed<float, 8>(a, s);
+            case 16: return launch_typed<float, 16>(a, s);
+            case 32: return launch_typed<float, 32>(a, s);
+        }
+    } else {
+        switch (a.E) {
+            case 8: return launch_typed<uint16_t, 8>(a, s);
+            case 16: return launch_typed<uint16_t, 16>(a, s);
+            case 32: return launch_typed<uint16_t, 32>(a, s);
+        }
+    }
+    return hipErrorInvalidValue;
+}
+
+hipError_t launch_zero_fill(void *ptr, size_t bytes, hipStream_t s) {
+    unsigned char *base = static_cast<unsigned char *>(ptr);
+    const size_t head = (16 - ((uintptr_t)base & 15)) & 15;
+    if (head) {
+        zero_fill_kernel<<<1, 64, 0, s>>>(nullptr, 0, base, head < bytes ? head : bytes);
+        if (head >= bytes) return hipGetLastError();
+    }
+    const size_t rest = bytes - head;
+    const size_t n16 = rest / 16;
+    const unsigned blocks = (unsigned)(n16 / 256 + 1 < 1024 ? n16 / 256 + 1 : 1024);
+    zero_fill_kernel<<<blocks, 256, 0, s>>>(reinterpret_cast<uint4 *>(base + head), n16,
+                                            base + head + n16 * 16, rest - n16 * 16);
+    return hipGetLastError();
+}
+
+}  // namespace kls

@@ -1,0 +1,134 @@
+/*
+ * klsample.h - C ABI of the MI355X (gfx950) fused token-sampling library.
+ *
+ * One call samples one token for each of B rows of a [B, V] logits matrix that is
+ * resident in device memory.  Per row it applies, in the reference's order:
+ *   repetition penalty            serving/sampling.py:47-49
+ *   presence/frequency penalties  (no reference counterpart; applied after the above)
+ *   greedy argmax when T == 0     serving/sampling.py:50-51
+ *   temperature, top-k, top-p     serving/sampling.py:53-59
+ *   the draw                      serving/sampling.py:60 (inverse CDF on a caller uniform)
+ *   log-softmax + top-N logprobs  serving/sampling.py:61-63
+ *
+ * Conventions: the caller owns every buffer (device pointers unless stated); the
+ * library never allocates, never synchronises the stream and never throws across
+ * this boundary.  Every argument is validated on the host before the first HIP
+ * call, so an invalid call returns a status without touching the device.
+ * Functions return KLSAMPLE_OK (0) or a negative status; klsample_last_error()
+ * then describes the failure (thread-local string).
+ */
+#ifndef KLSAMPLE_H
+#define KLSAMPLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define KLSAMPLE_ABI_VERSION 1
+
+/* status codes */
+#define KLSAMPLE_OK 0
+#define KLSAMPLE_ERR_INVALID_ARGUMENT (-1)
+#define KLSAMPLE_ERR_UNSUPPORTED_DTYPE (-2)
+#define KLSAMPLE_ERR_WORKSPACE (-3)
+#define KLSAMPLE_ERR_HIP (-4)
+
+/* logits element types */
+#define KLSAMPLE_FLOAT32 0
+#define KLSAMPLE_BFLOAT16 1
+
+/* klsample_row_params.flags: the reference's double-precision tests, evaluated by the
+ * caller on the original Python floats (an fp32 value alone cannot tell 0.99999999 < 1). */
+#define KLSAMPLE_ROW_GREEDY 1u            /* temperature == 0       serving/sampling.py:50 */
+#define KLSAMPLE_ROW_REPETITION 2u        /* repetition_penalty != 1 serving/sampling.py:47 */
+#define KLSAMPLE_ROW_PRESENCE_FREQUENCY 4u /* presence or frequency penalty != 0 */
+#define KLSAMPLE_ROW_TOP_P 8u             /* top_p < 1               serving/sampling.py:56 */
+
+/* klsample_batch.options */
+#define KLSAMPLE_OPT_FORCE_DENSE 1u       /* resolve every row on the multi-pass path (testing) */
+#define KLSAMPLE_OPT_SPLIT_COMBINE 2u     /* combine rows in a second launch instead of the last chunk */
+
+/* Per-row sampling parameters (32 bytes).  Mirrors SamplingParams
+ * (serving/sampling.py:8-15) plus presence/frequency and the row's uniform.
+ * Floats are the fp32 roundings of the Python values, which is what the reference's
+ * tensor-by-scalar operations use. */
+typedef struct klsample_row_params {
+    float temperature;
+    int32_t top_k;              /* 0 disables top-k; >= vocab keeps everything */
+    float top_p;
+    float repetition_penalty;
+    float presence_penalty;
+    float frequency_penalty;
+    float uniform;              /* U[0,1) driving the inverse-CDF draw (sampled rows) */
+    uint32_t flags;             /* KLSAMPLE_ROW_* */
+} klsample_row_params;
+
+/* Optional per-row diagnostics (32 bytes).  The kept set is
+ * { i : s_i > cut_score } U { i : s_i == cut_score and i <= cut_index } and its
+ * probabilities are exp(s_i - max_score - log_norm). */
+typedef struct klsample_row_info {
+    float max_score;
+    float cut_score;
+    int32_t cut_index;
+    int32_t kept;
+    double log_norm;
+    int32_t path;               /* 0: resolved from chunk candidates, 1: multi-pass row path */
+    int32_t mode;               /* 0 greedy, 1 top-k, 2 top-p only, 3 full distribution */
+} klsample_row_info;
+
+/* One batched sampling call. */
+typedef struct klsample_batch {
+    const void *logits;         /* [batch, row_stride] of dtype; rows read, never written */
+    int64_t row_stride;         /* elements between consecutive rows (>= vocab) */
+    int32_t dtype;              /* KLSAMPLE_FLOAT32 | KLSAMPLE_BFLOAT16 */
+    int32_t batch;              /* B >= 1 */
+    int32_t vocab;              /* V >= 1 */
+    int32_t num_logprobs;       /* N in [0, 256]: top-N logprobs per row */
+    int32_t max_top_k;          /* max over rows of top_k (0 if none); sizes candidate slots */
+    uint32_t options;           /* KLSAMPLE_OPT_* */
+    const klsample_row_params *params;      /* [batch] */
+    const int32_t *history_ids;             /* CSR token history; ids in [0, vocab) */
+    const int32_t *history_offsets;         /* [batch + 1]; NULL means no history */
+    int64_t *token_ids;                     /* [batch] out */
+    float *logprobs;                        /* [batch] out: log-softmax of the sampled token */
+    int32_t *top_ids;                       /* [batch * num_logprobs] out, or NULL if N == 0 */
+    float *top_logprobs;                    /* [batch * num_logprobs] out, or NULL if N == 0 */
+    float *probs;                           /* optional [batch * vocab] out: final probabilities */
+    klsample_row_info *row_info;            /* optional [batch] out */
+    void *workspace;                        /* device scratch, see klsample_workspace_size */
+    size_t workspace_bytes;
+} klsample_batch;
+
+/* ABI version of the loaded library (KLSAMPLE_ABI_VERSION). */
+int klsample_abi_version(void);
+
+/* Bytes of device workspace a call with these sizes needs.  Writes *bytes and
+ * returns KLSAMPLE_OK, or a negative status for invalid sizes.
+ * No reference counterpart: the reference allocates inside torch ops per call. */
+int klsample_workspace_size(int32_t batch, int32_t vocab, int32_t dtype, int32_t max_top_k,
+                            int32_t num_logprobs, size_t *bytes);
+
+/* Zero-fill a workspace before its first use (enqueued on `stream`, a hipStream_t).
+ * Calls leave the workspace in the state they found it, so this is needed once per
+ * allocation. */
+int klsample_workspace_init(void *workspace, size_t workspace_bytes, void *stream);
+
+/* Sample one token per row; enqueued on `stream` (a hipStream_t, NULL = default).
+ * Replaces Sampler.sample (serving/sampling.py:43-63), batched over rows: for row b
+ * it computes what Sampler(params_b).sample(logits[b], history_b) returns, with the
+ * multinomial draw of serving/sampling.py:60 replaced by the inverse CDF on
+ * params[b].uniform: the smallest index i whose cumulative probability (vocab order)
+ * exceeds uniform * total. */
+int klsample_run(const klsample_batch *batch, void *stream);
+
+/* Description of the last failure on this thread ("" if none). */
+const char *klsample_last_error(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* KLSAMPLE_H */

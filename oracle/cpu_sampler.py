@@ -1,0 +1,201 @@
+"""CPU restatement of the reference sampler, used as the parity oracle.
+
+TEST INFRASTRUCTURE ONLY (see ``oracle/__init__.py``).
+
+The reference (``serving/sampling.py:44-63``) processes one row per call with stock
+PyTorch CPU operations.  This module runs the same operations in the same order,
+so that on the same fp32 inputs it produces the same scores bit for bit, and adds:
+
+* presence and frequency penalties, which the reference lacks (its
+  ``SamplingParams`` stops at ``logprobs``, ``serving/sampling.py:8-15``), applied
+  after the repetition penalty over the same history;
+* ``uniform`` mode, where the multinomial draw (``serving/sampling.py:60``) becomes
+  an inverse CDF on a caller-supplied uniform ``u``;
+* per-row diagnostics that classify a row as a *boundary row* (the top-p crossing,
+  a value tie or the CDF step lies within ``1e-6`` of the cut), which is the only
+  class of row whose token id may differ from a GPU implementation.
+
+PyTorch facts this restatement relies on (probed on the installed torch CPU build):
+``tensor / python_float`` is IEEE fp32 division by ``fp32(value)``;
+``tensor * python_float`` multiplies by ``fp32(value)``; ``tensor > python_float``
+compares against ``fp32(value)``; ``cumsum`` on fp32 accumulates in double and
+rounds each element to fp32.
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass, field
+
+import numpy as np
+import torch
+
+BOUNDARY_EPS = 1e-6
+
+
+@dataclass
+class OracleRow:
+    """Result of one restated ``Sampler.sample`` call plus diagnostics."""
+
+    token_id: int
+    logprob: float
+    top_logprobs: tuple
+    stopped: bool
+    greedy: bool
+    probs: torch.Tensor | None = None      # vector handed to the draw (sampled rows)
+    scores: torch.Tensor | None = None     # final scores (after penalties, T, top-k/p)
+    kept: int = 0                          # number of finite final scores
+    # boundary classification (sampled rows only)
+    topp_margin: float = math.inf          # |excl_cumsum - p| nearest the cut
+    topp_tie: bool = False                 # a value tie straddles the top-p cut
+    cdf_margin: float = math.inf           # |cdf step - u*Z| / Z nearest the token
+    notes: list = field(default_factory=list)
+
+    @property
+    def boundary(self) -> bool:
+        return (self.topp_margin < BOUNDARY_EPS or self.topp_tie
+                or self.cdf_margin < BOUNDARY_EPS)
+
+
+def normalize_history(history, vocab: int) -> np.ndarray:
+    """History ids as int64 in ``[0, vocab)``.
+
+    The reference indexes ``scores[ids]`` with the raw ids
+    (``serving/sampling.py:48-49``): a negative id counts from the end, and an id
+    outside ``[-vocab, vocab)`` raises ``IndexError``.
+    """
+    ids = np.asarray(list(history), dtype=np.int64).reshape(-1)
+    if ids.size and (ids.min() < -vocab or ids.max() >= vocab):
+        bad = ids[(ids < -vocab) | (ids >= vocab)][0]
+        raise IndexError(f'index {int(bad)} is out of bounds for dimension 0 with size {vocab}')
+    return np.where(ids < 0, ids + vocab, ids)
+
+
+def inverse_cdf(probs: torch.Tensor, u: float) -> int:
+    """Smallest vocab index ``i`` with ``sum(probs[:i+1]) > u * sum(probs)``.
+
+    Replaces ``torch.multinomial(probs, 1, generator)`` (``serving/sampling.py:60``)
+    with a draw driven by one caller-supplied uniform ``u`` in ``[0, 1)``.  The
+    cumulative sum runs in float64 in vocab order.  If rounding leaves no index
+    above the target, the last index with non-zero probability is returned.
+    """
+    p = probs.detach().double().numpy()
+    c = np.cumsum(p)
+    target = float(u) * c[-1]
+    i = int(np.searchsorted(c, target, side='right'))
+    if i >= p.size:
+        i = int(np.flatnonzero(p > 0)[-1])
+    return i
+
+
+def _apply_penalties(scores: torch.Tensor, ids: np.ndarray, params) -> None:
+    """Repetition penalty (``serving/sampling.py:47-49``), then presence/frequency."""
+    r = params.repetition_penalty
+    if r != 1 and ids.size:
+        # serving/sampling.py:48 builds the sorted distinct ids; after normalising
+        # negative ids the duplicates collapse to the same element, which the
+        # reference also updates once (every copy writes the same value).
+        uniq = torch.from_numpy(np.unique(ids))
+        sel = scores[uniq]
+        scores[uniq] = torch.where(sel < 0, sel * r, sel / r)
+    a = getattr(params, 'presence_penalty', 0.0)
+    b = getattr(params, 'frequency_penalty', 0.0)
+    if (a != 0 or b != 0) and ids.size:
+        uniq, counts = np.unique(ids, return_counts=True)
+        idx = torch.from_numpy(uniq)
+        # closed form, three fp32 roundings, no fused multiply-add:
+        #   t = fp32(beta * count); t = fp32(t + alpha); s = fp32(s - t)
+        t = torch.from_numpy(counts.astype(np.float32)) * b
+        t = t + a
+        scores[idx] = scores[idx] - t
+
+
+def restated_sample(logits: torch.Tensor, history=(), params=None, *, u: float | None = None,
+                    generator: torch.Generator | None = None, diagnostics: bool = True) -> OracleRow:
+    """One reference ``Sampler.sample`` call (``serving/sampling.py:44-63``).
+
+    ``u`` selects uniform mode (inverse CDF); otherwise ``generator`` drives
+    ``torch.multinomial`` exactly as the reference does.
+    """
+    if logits.ndim != 1 or not logits.is_floating_point():        # :45
+        raise ValueError('logits must be a floating vector')
+    p = params
+    scores = logits.detach().to('cpu').float().clone()             # :46
+    vocab = scores.numel()
+    ids = normalize_history(history, vocab)
+    _apply_penalties(scores, ids, p)                               # :47-49 (+ presence/frequency)
+    row = OracleRow(0, 0.0, (), False, p.temperature == 0)
+    if p.temperature == 0:                                         # :50-51
+        token = int(scores.argmax())
+    else:
+        scores /= p.temperature                                    # :53
+        if p.top_k:                                                # :54-55
+            k = min(p.top_k, vocab)
+            cutoff = scores.topk(k).values[-1]
+            scores.masked_fill_(scores < cutoff, -torch.inf)
+        if p.top_p < 1:                                            # :56-59
+            ordered, index = scores.sort(descending=True)
+            probabilities = ordered.softmax(0)
+            excl = probabilities.cumsum(0) - probabilities
+            remove = excl > p.top_p
+            if diagnostics:
+                _topp_diagnostics(row, ordered, excl, remove, p.top_p)
+            scores[index[remove]] = -torch.inf
+        probs = scores.softmax(0)                                  # :60
+        row.probs = probs
+        if u is not None:
+            token = inverse_cdf(probs, u)
+            if diagnostics:
+                _cdf_diagnostics(row, probs, token, u)
+        else:
+            token = int(torch.multinomial(probs, 1, generator=generator))
+    log_probabilities = scores.log_softmax(0)                      # :61
+    count = min(p.logprobs, vocab)
+    top = () if not count else tuple(                              # :62
+        (int(i), float(v)) for v, i in zip(*log_probabilities.topk(count)))
+    row.token_id = token
+    row.logprob = float(log_probabilities[token])                  # :63
+    row.top_logprobs = top
+    row.stopped = token in p.stop_token_ids
+    row.scores = scores
+    row.kept = int(torch.isfinite(scores).sum()) if p.temperature != 0 else vocab
+    return row
+
+
+def _topp_diagnostics(row: OracleRow, ordered, excl, remove, top_p) -> None:
+    """Distance of the top-p decision from its cut, and ties across the cut."""
+    p32 = float(np.float32(top_p))
+    e = excl.double().numpy()
+    rm = remove.numpy()
+    n = e.size
+    first_removed = int(np.argmax(rm)) if rm.any() else n
+    margins = []
+    for j in (first_removed - 1, first_removed):
+        if 0 <= j < n and np.isfinite(ordered[j].item()):
+            margins.append(abs(e[j] - p32))
+    row.topp_margin = min(margins) if margins else math.inf
+    if 0 < first_removed < n:
+        row.topp_tie = bool(ordered[first_removed - 1].item() == ordered[first_removed].item())
+
+
+def _cdf_diagnostics(row: OracleRow, probs, token: int, u: float) -> None:
+    """Relative distance of ``u * Z`` from the CDF steps around the chosen token."""
+    c = np.cumsum(probs.double().numpy())
+    z = c[-1]
+    target = float(u) * z
+    steps = [c[token]]
+    if token > 0:
+        steps.append(c[token - 1])
+    row.cdf_margin = min(abs(s - target) for s in steps) / z
+
+
+def sample_rows(logits2d: torch.Tensor, histories, params_list, uniforms=None,
+                generators=None, diagnostics: bool = True) -> list[OracleRow]:
+    """Row loop over a ``[B, V]`` batch, one reference call per row (as
+    ``serving/engine.py:92-96`` calls the sampler once per request row)."""
+    out = []
+    for b in range(logits2d.shape[0]):
+        u = None if uniforms is None else float(uniforms[b])
+        g = None if generators is None else generators[b]
+        out.append(restated_sample(logits2d[b], histories[b] if histories is not None else (),
+                                   params_list[b], u=u, generator=g, diagnostics=diagnostics))
+    return out

@@ -1,0 +1,145 @@
+"""Shared test helpers: golden-vector decoding and the parity comparison."""
+from __future__ import annotations
+
+import base64
+import json
+import math
+from dataclasses import dataclass, field
+from pathlib import Path
+
+import numpy as np
+import torch
+
+GOLDEN = Path(__file__).resolve().parent / 'golden' / 'reference_vectors.json'
+
+
+@dataclass(frozen=True)
+class GoldenParams:
+    """Plain parameter record (the fields ``SamplingParams`` has)."""
+
+    temperature: float = 0.0
+    top_k: int = 0
+    top_p: float = 1.0
+    repetition_penalty: float = 1.0
+    stop_token_ids: frozenset = frozenset()
+    seed: int = 0
+    logprobs: int = 0
+    presence_penalty: float = 0.0
+    frequency_penalty: float = 0.0
+
+
+def _arr(text, dtype):
+    return np.frombuffer(base64.b64decode(text), dtype=dtype).copy()
+
+
+def _num(x):
+    return float(x) if not isinstance(x, str) else float(x)
+
+
+def golden_cases():
+    data = json.loads(GOLDEN.read_text())
+    out = []
+    for c in data['cases']:
+        kw = dict(c['params'])
+        kw['stop_token_ids'] = frozenset(kw.get('stop_token_ids', []))
+        exp = c['expected']
+        probs = None
+        if exp['probs_nonzero'] is not None:
+            probs = np.zeros(c['vocab'], dtype=np.float32)
+            idx = _arr(exp['probs_nonzero']['index_i32'], '<i4')
+            probs[idx] = _arr(exp['probs_nonzero']['value_f32'], '<f4')
+        out.append(dict(
+            name=c['name'], logits=torch.from_numpy(_arr(c['logits_f32'], '<f4')), history=c['history'],
+            params=GoldenParams(**kw), u=c['u'], token=exp['token_id'], logprob=_num(exp['logprob']),
+            top=[(i, _num(v)) for i, v in exp['top_logprobs']], stopped=exp['stopped'], probs=probs))
+    return out
+
+
+def close(a: float, b: float, tol: float = 1e-5) -> bool:
+    if math.isinf(a) or math.isinf(b) or math.isnan(a) or math.isnan(b):
+        return (a == b) or (math.isnan(a) and math.isnan(b))
+    return abs(a - b) <= tol * max(1.0, abs(b))
+
+
+def top_matches(got, want, tol: float = 1e-5) -> bool:
+    """Top-logprob lists agree: same length, values within ``tol``, and the same ids
+    except among entries tied in value (their order is implementation-defined) and
+    among -inf entries (their ids are implementation-defined)."""
+    if len(got) != len(want):
+        return False
+    for (gi, gv), (wi, wv) in zip(got, want):
+        if not close(gv, wv, tol):
+            return False
+    finite_w = {}
+    for i, v in want:
+        if math.isfinite(v):
+            finite_w.setdefault(round(v, 5), set()).add(i)
+    finite_g = {}
+    for i, v in got:
+        if math.isfinite(v):
+            finite_g.setdefault(round(v, 5), set()).add(i)
+    last = min(finite_w) if finite_w else None
+    for key, ids in finite_w.items():
+        if key == last:
+            continue  # the last tied group may be cut at a different member
+        if finite_g.get(key) != ids:
+            return False
+    return True
+
+
+@dataclass
+class ParityReport:
+    rows: int = 0
+    exact: int = 0
+    boundary_rows: int = 0
+    boundary_mismatches: int = 0
+    failures: list = field(default_factory=list)
+
+    def ok(self) -> bool:
+        return not self.failures
+
+
+def compare(out, oracle_rows, params_list, *, tol: float = 1e-5, probs=None, check_top: bool = True) -> ParityReport:
+    """Row-by-row parity of a GPU call against oracle rows (uniform mode).
+
+    Token ids must be equal; a sampled row may differ only if the oracle classes it as a
+    boundary row (top-p cut or CDF step within 1e-6, or a value tie across the top-p
+    cut).  Logprobs must agree within ``tol`` (relative, floor 1); the number of kept
+    tokens must agree except on boundary rows; probabilities (if given) within ``tol``
+    relative on the kept set."""
+    rep = ParityReport()
+    for b, (o, p) in enumerate(zip(oracle_rows, params_list)):
+        rep.rows += 1
+        tok = int(out.tokens[b])
+        rep.boundary_rows += int(o.boundary)
+        if tok != o.token_id:
+            if o.boundary and not o.greedy:
+                rep.boundary_mismatches += 1
+                continue
+            rep.failures.append(f'row {b}: token {tok} != oracle {o.token_id} (greedy={o.greedy}, '
+                                f'topp_margin={o.topp_margin:.3g}, cdf_margin={o.cdf_margin:.3g})')
+            continue
+        rep.exact += 1
+        if not close(float(out.logprobs[b]), o.logprob, tol):
+            rep.failures.append(f'row {b}: logprob {float(out.logprobs[b])!r} != oracle {o.logprob!r}')
+        if out.info is not None and not o.greedy and not o.boundary:
+            if int(out.info['kept'][b]) != o.kept:
+                rep.failures.append(f'row {b}: kept {int(out.info["kept"][b])} != oracle {o.kept}')
+        if check_top and p.logprobs:
+            got = out.top(b, p.logprobs)
+            if not top_matches(got, list(o.top_logprobs), tol):
+                rep.failures.append(f'row {b}: top logprobs {got[:4]}... != oracle {list(o.top_logprobs)[:4]}...')
+        if probs is not None and o.probs is not None and not o.boundary:
+            # probabilities below 1e-30 are compared as zero: fp32 softmax values that
+            # small are subnormal in the reference and carry no relative precision
+            want = o.probs.numpy().astype(np.float64)
+            got = probs[b].astype(np.float64)
+            if not np.array_equal(want > 1e-30, got > 1e-30):
+                rep.failures.append(f'row {b}: kept support differs ({int((want > 1e-30).sum())} vs '
+                                    f'{int((got > 1e-30).sum())})')
+            else:
+                m = want > 1e-30
+                rel = np.abs(got[m] - want[m]) / want[m]
+                if rel.size and rel.max() > tol:
+                    rep.failures.append(f'row {b}: probability rel err {rel.max():.3g}')
+    return rep

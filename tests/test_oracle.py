@@ -1,0 +1,232 @@
+"""Pinning the CPU oracle (CPU only).
+
+The oracle restates serving/sampling.py:44-63.  Each check below is independent of the
+oracle's own code: the reference's known-answer test, vectors written by running the
+reference sampler, or a closed form evaluated here with numpy.  Each is chosen so a
+plausible slip (penalty sign, strict vs non-strict cut, dropped term, wrong rounding,
+off-by-one in the CDF) changes the answer."""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import GoldenParams, close, golden_cases
+from oracle.cpu_sampler import inverse_cdf, normalize_history, restated_sample, sample_rows
+
+P = GoldenParams
+CASES = golden_cases()
+
+
+def test_reference_known_answer_test():
+    # serving/test_serving.py:101-107
+    params = P(temperature=.8, top_k=3, top_p=.9, repetition_penalty=1.1, stop_token_ids=frozenset({2}),
+               seed=7, logprobs=2)
+    logits = torch.tensor([0., 1., 3., 2.])
+    a = restated_sample(logits, [2], params, u=0.5)
+    b = restated_sample(logits, [2], params, u=0.5)
+    assert (a.token_id, a.logprob, a.top_logprobs, a.stopped) == (b.token_id, b.logprob, b.top_logprobs, b.stopped)
+    assert len(a.top_logprobs) == 2
+    greedy = restated_sample(logits, (), P(stop_token_ids=frozenset({2})))
+    assert greedy.token_id == 2 and greedy.stopped
+
+
+def test_known_answer_hand_derived_values():
+    # numpy fp32 by hand: after r=1.1 on id 2 -> [0, 1, 2.7272727, 2]; /0.8 ->
+    # [0, 1.25, 3.409091, 2.5]; k=3 drops id 0; top-p .9 drops id 1 (exclusive mass .924)
+    params = P(temperature=.8, top_k=3, top_p=.9, repetition_penalty=1.1, logprobs=2)
+    row = restated_sample(torch.tensor([0., 1., 3., 2.]), [2], params, u=0.5)
+    probs = row.probs.numpy()
+    assert probs[0] == 0 and probs[1] == 0
+    assert probs[2] == pytest.approx(0.71281412, abs=1e-7)
+    assert probs[3] == pytest.approx(0.28718588, abs=1e-7)
+    assert dict(row.top_logprobs)[2] == pytest.approx(-0.33853459, abs=1e-7)
+    assert dict(row.top_logprobs)[3] == pytest.approx(-1.24762559, abs=1e-7)
+    assert restated_sample(torch.tensor([0., 1., 3., 2.]), [2], params, u=0.7128).token_id == 2
+    assert restated_sample(torch.tensor([0., 1., 3., 2.]), [2], params, u=0.7129).token_id == 3
+
+
+@pytest.mark.parametrize('case', CASES, ids=[c['name'] for c in CASES])
+def test_reference_vectors(case):
+    """Vectors written by running the reference sampler (tests/golden/make_reference_vectors.py)."""
+    row = restated_sample(case['logits'], case['history'], case['params'], u=case['u'])
+    assert row.token_id == case['token']
+    assert row.stopped == case['stopped']
+    assert close(row.logprob, case['logprob'], 1e-6)
+    assert len(row.top_logprobs) == len(case['top'])
+    for (gi, gv), (wi, wv) in zip(row.top_logprobs, case['top']):
+        assert close(gv, wv, 1e-6)
+        if math.isfinite(wv):
+            assert gi == wi
+    if case['probs'] is None:
+        assert row.probs is None
+    else:
+        got = row.probs.numpy()
+        np.testing.assert_array_equal(got > 0, case['probs'] > 0)
+        np.testing.assert_allclose(got, case['probs'], rtol=1e-6, atol=0)
+
+
+# ---- closed forms -----------------------------------------------------------------------
+
+def _numpy_penalised(x, history, r, a=0.0, b=0.0):
+    """fp32 closed form: repetition on distinct ids (multiply negatives, divide the rest),
+    then s - fp32(fp32(b*count) + a)."""
+    s = x.astype(np.float32).copy()
+    ids, counts = np.unique(np.asarray(history, dtype=np.int64), return_counts=True)
+    if r != 1 and ids.size:
+        rr = np.float32(r)
+        v = s[ids]
+        s[ids] = np.where(v < 0, v * rr, v / rr).astype(np.float32)
+    if (a != 0 or b != 0) and ids.size:
+        t = (np.float32(b) * counts.astype(np.float32)).astype(np.float32)
+        t = (t + np.float32(a)).astype(np.float32)
+        s[ids] = (s[ids] - t).astype(np.float32)
+    return s
+
+
+def test_repetition_penalty_closed_form():
+    rng = np.random.default_rng(1)
+    x = (rng.standard_normal(300) * 3).astype(np.float32)
+    x[:3] = [0.0, -0.0, -2.5]
+    hist = list(rng.integers(0, 300, 80)) + [0, 1, 2, 2, 2]
+    for r in (1.1, 1.7, 0.6):
+        row = restated_sample(torch.from_numpy(x), hist, P(repetition_penalty=r))
+        np.testing.assert_array_equal(row.scores.numpy(), _numpy_penalised(x, hist, r))
+    # applied once per distinct id, and multiplying (not dividing) negative scores
+    row = restated_sample(torch.tensor([-2.0, 2.0]), [0, 0, 1], P(repetition_penalty=2.0))
+    assert row.scores.tolist() == [-4.0, 1.0]
+
+
+def test_presence_frequency_closed_form_and_zero_invariant():
+    rng = np.random.default_rng(2)
+    x = (rng.standard_normal(500) * 2).astype(np.float32)
+    hist = list(rng.integers(0, 500, 200)) + [7] * 9
+    for a, b in ((0.5, 0.3), (0.0, 0.7), (-0.4, 0.0)):
+        row = restated_sample(torch.from_numpy(x), hist, P(repetition_penalty=1.2, presence_penalty=a,
+                                                          frequency_penalty=b))
+        np.testing.assert_array_equal(row.scores.numpy(), _numpy_penalised(x, hist, 1.2, a, b))
+    # brute-force count on a tiny history: id 1 seen 3 times, id 0 once
+    row = restated_sample(torch.tensor([1.0, 1.0, 1.0]), [1, 0, 1, 1], P(presence_penalty=0.5, frequency_penalty=0.25))
+    assert row.scores.tolist() == [1.0 - (0.25 * 1 + 0.5), 1.0 - (0.25 * 3 + 0.5), 1.0]
+    # alpha == beta == 0 reproduces the reference exactly
+    base = restated_sample(torch.from_numpy(x), hist, P(temperature=0.9, top_k=30, repetition_penalty=1.3), u=0.4)
+    zero = restated_sample(torch.from_numpy(x), hist, P(temperature=0.9, top_k=30, repetition_penalty=1.3,
+                                                       presence_penalty=0.0, frequency_penalty=0.0), u=0.4)
+    assert torch.equal(base.scores, zero.scores) and base.token_id == zero.token_id
+
+
+def test_temperature_is_ieee_fp32_division():
+    x = (np.random.default_rng(7).standard_normal(4096) * 5).astype(np.float32)
+    row = restated_sample(torch.from_numpy(x), (), P(temperature=0.7), u=0.3)
+    np.testing.assert_array_equal(row.scores.numpy(), x / np.float32(0.7))
+    # neither a reciprocal multiply nor a double-precision quotient gives these values
+    assert not np.array_equal(row.scores.numpy(), x * np.float32(1 / 0.7))
+    assert not np.array_equal(row.scores.numpy(), (x.astype(np.float64) / 0.7).astype(np.float32))
+
+
+def test_topk_threshold_with_multiplicity_brute_force():
+    rng = np.random.default_rng(3)
+    for trial in range(30):
+        v = int(rng.integers(2, 40))
+        x = rng.integers(-4, 5, v).astype(np.float32)  # many ties
+        k = int(rng.integers(1, v + 3))
+        row = restated_sample(torch.from_numpy(x), (), P(temperature=1.0, top_k=k), u=0.5)
+        kk = min(k, v)
+        cutoff = np.sort(x)[::-1][kk - 1]
+        np.testing.assert_array_equal(np.isfinite(row.scores.numpy()), x >= cutoff)
+
+
+def test_topp_distinct_values_closed_form():
+    rng = np.random.default_rng(4)
+    for trial in range(40):
+        v = int(rng.integers(2, 60))
+        x = rng.permutation(np.linspace(-3, 3, v)).astype(np.float32)
+        p = float(rng.uniform(0.05, 0.99))
+        row = restated_sample(torch.from_numpy(x), (), P(temperature=1.0, top_p=p), u=0.5)
+        order = np.argsort(-x.astype(np.float64))
+        w = np.exp(x[order].astype(np.float64) - x.max())
+        excl = (np.cumsum(w) - w) / w.sum()
+        keep = np.zeros(v, bool)
+        keep[order[excl <= np.float32(p)]] = True
+        if np.min(np.abs(excl - np.float32(p))) < 1e-6:
+            continue  # within the boundary tolerance fp32 rounding decides
+        np.testing.assert_array_equal(np.isfinite(row.scores.numpy()), keep)
+        assert keep[order[0]]  # the crossing token is kept: never empty
+
+
+def test_logprob_is_log_softmax_of_final_scores():
+    rng = np.random.default_rng(5)
+    x = (rng.standard_normal(1000) * 2).astype(np.float32)
+    row = restated_sample(torch.from_numpy(x), (), P(temperature=0.8, top_k=50, top_p=0.9, logprobs=5), u=0.6)
+    s = row.scores.numpy().astype(np.float64)
+    f = np.isfinite(s)
+    lse = s[f].max() + np.log(np.exp(s[f] - s[f].max()).sum())
+    assert row.logprob == pytest.approx(s[row.token_id] - lse, abs=2e-6)
+    assert [i for i, _ in row.top_logprobs] == list(np.argsort(-s)[:5])
+    greedy = restated_sample(torch.from_numpy(x), (), P(logprobs=1))
+    lse_all = x.max() + np.log(np.exp(x.astype(np.float64) - x.max()).sum())
+    assert greedy.logprob == pytest.approx(x.max() - lse_all, abs=2e-6)
+
+
+def test_greedy_takes_lowest_index_of_ties():
+    assert restated_sample(torch.tensor([1., 5., 2., 5.]), (), P()).token_id == 1
+    assert restated_sample(torch.tensor([-1., -1., -1.]), (), P()).token_id == 0
+
+
+def test_inverse_cdf_brute_force_and_monotone():
+    rng = np.random.default_rng(6)
+    for trial in range(50):
+        v = int(rng.integers(1, 30))
+        p = rng.random(v).astype(np.float32)
+        p[rng.random(v) < 0.3] = 0
+        if p.sum() == 0:
+            p[int(rng.integers(0, v))] = 1.0
+        u = float(np.float32(rng.random()))
+        total = float(np.sum(p.astype(np.float64)))
+        acc, want = 0.0, None
+        for i in range(v):
+            acc += float(p[i])
+            if acc > u * total:
+                want = i
+                break
+        if want is None:
+            want = int(np.flatnonzero(p)[-1])
+        assert inverse_cdf(torch.from_numpy(p), u) == want
+        assert p[want] > 0
+    p = torch.tensor([0.1, 0.0, 0.4, 0.5])
+    toks = [inverse_cdf(p, u) for u in np.linspace(0, 0.999, 200)]
+    assert toks == sorted(toks) and set(toks) == {0, 2, 3}
+
+
+def test_history_normalisation_matches_indexing():
+    assert normalize_history([-1, 0, 3], 4).tolist() == [3, 0, 3]
+    with pytest.raises(IndexError):
+        normalize_history([4], 4)
+    with pytest.raises(IndexError):
+        normalize_history([-5], 4)
+
+
+def test_boundary_classification():
+    # exact value tie straddling the top-p cut
+    row = restated_sample(torch.tensor([2., 1., 1., 0.]), (), P(temperature=1.0, top_p=0.7), u=0.5)
+    assert row.topp_tie and row.boundary
+    # far from every cut
+    row = restated_sample(torch.tensor([3., 1., 0.5, 0.]), (), P(temperature=1.0, top_p=0.5), u=0.2)
+    assert not row.boundary
+
+
+def test_faithful_mode_is_the_reference_draw():
+    """Faithful mode draws with torch.multinomial from the seeded generator, as
+    serving/sampling.py:60 does; equal seeds give equal tokens."""
+    x = torch.randn(5000, generator=torch.Generator().manual_seed(0))
+    params = P(temperature=1.0, top_k=0, top_p=0.95, seed=11)
+    g1, g2 = torch.Generator().manual_seed(11), torch.Generator().manual_seed(11)
+    a = [restated_sample(x, (), params, generator=g1).token_id for _ in range(5)]
+    b = [restated_sample(x, (), params, generator=g2).token_id for _ in range(5)]
+    assert a == b
+
+
+def test_sample_rows_loops_rows():
+    x = torch.tensor([[0., 1., 3., 2.], [3., 2., 1., 0.]])
+    rows = sample_rows(x, [[2], []], [P(repetition_penalty=1.1), P()], None)
+    assert [r.token_id for r in rows] == [2, 0]

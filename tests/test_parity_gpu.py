@@ -1,0 +1,237 @@
+"""Parity of the HIP sampling path with the CPU oracle (MI355X only).
+
+Token ids must be bit-exact except on boundary rows (top-p cut, value tie across the
+cut, or CDF step within 1e-6), logprobs within 1e-5, kept sets equal, and the final
+probabilities within 1e-5 relative."""
+import math
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import close, compare, golden_cases
+from klsample import SamplingParams, _lib, workloads
+from klsample.runner import runner_for
+from oracle.cpu_sampler import restated_sample, sample_rows
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device('cuda', 0)
+TOL = 1e-5
+
+
+def say(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def run(logits, params, histories, uniforms, *, options=0, probs=False, n=None):
+    n = max((p.logprobs for p in params), default=0) if n is None else n
+    say(f'  klsample_run B={logits.shape[0]} V={logits.shape[-1]} dtype={logits.dtype} N={n} options={options}')
+    out = runner_for(DEV).run(logits.to(DEV), params, histories, uniforms, n, options=options,
+                              want_probs=probs, want_info=True)
+    torch.cuda.synchronize()
+    return out
+
+
+def check(out, rows, params, probs=False, max_boundary_frac=0.02):
+    rep = compare(out, rows, params, tol=TOL, probs=out.probs.cpu().numpy() if probs else None)
+    say(f'  rows={rep.rows} exact={rep.exact} boundary_rows={rep.boundary_rows} '
+        f'boundary_mismatches={rep.boundary_mismatches} failures={len(rep.failures)}')
+    assert rep.ok(), '\n'.join(rep.failures[:20])
+    assert rep.boundary_mismatches <= max(1, int(max_boundary_frac * rep.rows))
+    return rep
+
+
+def _with_logprobs(w, n):
+    ps = [SamplingParams(p.temperature, p.top_k, p.top_p, p.repetition_penalty, p.stop_token_ids, p.seed, n,
+                         p.presence_penalty, p.frequency_penalty) for p in w.params]
+    return workloads.Workload(w.name, w.logits, ps, w.histories, w.uniforms)
+
+
+# ---- the configured workloads -------------------------------------------------------------
+
+@pytest.mark.parametrize('name,batch,n,probs', [
+    ('cpu_reference_b8', None, 0, True),
+    ('cpu_reference_b8', None, 5, False),
+    ('latency_b1', None, 20, True),
+    ('latency_b1_greedy', None, 3, True),
+    ('mixed_b64', None, 5, False),
+    ('throughput_b256_v128256', None, 0, False),
+    ('throughput_b256_v151936', None, 0, False),
+    ('tie_stress_b1024', None, 0, False),
+])
+def test_workload_parity(name, batch, n, probs):
+    say(f'workload {name} batch={batch} logprobs={n}')
+    w = _with_logprobs(workloads.make(name, batch=batch), n)
+    rows = sample_rows(w.logits, w.histories, w.params, w.uniforms)
+    out = run(w.logits, w.params, w.histories, w.uniforms, probs=probs)
+    check(out, rows, w.params, probs=probs)
+
+
+@pytest.mark.parametrize('name,batch', [
+    ('cpu_reference_b8', None),
+    ('latency_b1', None),
+    ('mixed_b64', 16),
+    ('throughput_b256_v151936', 8),
+    ('tie_stress_b1024', 16),
+])
+def test_row_path_parity(name, batch):
+    """Every row forced through the multi-pass row path (dense_kernel)."""
+    say(f'row path {name} batch={batch}')
+    w = _with_logprobs(workloads.make(name, batch=batch), 4)
+    rows = sample_rows(w.logits, w.histories, w.params, w.uniforms)
+    out = run(w.logits, w.params, w.histories, w.uniforms, options=_lib.OPT_FORCE_DENSE, probs=True)
+    assert (out.info['path'] == 1).all()
+    check(out, rows, w.params, probs=True)
+
+
+@pytest.mark.parametrize('name,batch', [('cpu_reference_b8', None), ('mixed_b64', 16)])
+def test_split_combine_matches_fused(name, batch):
+    say(f'split combine {name} batch={batch}')
+    w = _with_logprobs(workloads.make(name, batch=batch), 3)
+    a = run(w.logits, w.params, w.histories, w.uniforms)
+    b = run(w.logits, w.params, w.histories, w.uniforms, options=_lib.OPT_SPLIT_COMBINE)
+    assert np.array_equal(a.tokens, b.tokens)
+    assert np.array_equal(a.logprobs, b.logprobs)
+    assert np.array_equal(a.top_ids, b.top_ids)
+
+
+def test_repeated_calls_are_deterministic():
+    say('determinism mixed_b64[:16] x3')
+    w = workloads.make('mixed_b64', batch=16)
+    outs = [run(w.logits, w.params, w.histories, w.uniforms) for _ in range(3)]
+    for o in outs[1:]:
+        assert np.array_equal(o.tokens, outs[0].tokens)
+        assert np.array_equal(o.logprobs, outs[0].logprobs)
+
+
+# ---- vectors written by the reference sampler ----------------------------------------------
+
+CASES = golden_cases()
+
+
+@pytest.mark.parametrize('case', CASES, ids=[c['name'] for c in CASES])
+def test_reference_vectors_on_gpu(case):
+    say(f'golden {case["name"]}')
+    p = case['params']
+    params = SamplingParams(p.temperature, p.top_k, p.top_p, p.repetition_penalty, p.stop_token_ids, p.seed,
+                            p.logprobs)
+    oracle_row = restated_sample(case['logits'], case['history'], params, u=case['u'])
+    out = run(case['logits'][None, :], [params], [case['history']], [case['u']], probs=True)
+    tok = int(out.tokens[0])
+    if tok != case['token']:
+        assert oracle_row.boundary and not oracle_row.greedy, (tok, case['token'])
+        return
+    assert close(float(out.logprobs[0]), case['logprob'], TOL)
+    assert (tok in params.stop_token_ids) == case['stopped']
+    got_top = out.top(0, params.logprobs)
+    assert len(got_top) == len(case['top'])
+    for (gi, gv), (wi, wv) in zip(got_top, case['top']):
+        assert close(gv, wv, TOL)
+    if case['probs'] is not None and not oracle_row.boundary:
+        got = out.probs.cpu().numpy()[0]
+        np.testing.assert_array_equal(got > 0, case['probs'] > 0)
+        m = case['probs'] > 1e-30
+        np.testing.assert_allclose(got[m], case['probs'][m], rtol=TOL, atol=0)
+
+
+# ---- edge cases ------------------------------------------------------------------------------
+
+def _random_params(rng, kind):
+    if kind == 'greedy':
+        return SamplingParams(repetition_penalty=1.3, logprobs=4)
+    if kind == 'topk':
+        return SamplingParams(temperature=0.8, top_k=int(rng.integers(1, 60)), top_p=0.9, repetition_penalty=1.2,
+                              logprobs=4, presence_penalty=0.4, frequency_penalty=0.2)
+    if kind == 'topp':
+        return SamplingParams(temperature=1.1, top_p=float(rng.uniform(0.3, 0.99)), repetition_penalty=0.9,
+                              logprobs=4)
+    return SamplingParams(temperature=0.6, logprobs=4, frequency_penalty=0.5)
+
+
+@pytest.mark.parametrize('vocab', [1, 2, 3, 5, 17, 100, 1000, 4097, 10007, 70001])
+@pytest.mark.parametrize('dtype', [torch.float32, torch.bfloat16])
+def test_vocab_sizes_and_modes(vocab, dtype):
+    say(f'edge vocab={vocab} dtype={dtype}')
+    rng = np.random.default_rng(vocab)
+    kinds = ['greedy', 'topk', 'topp', 'full'] * 2
+    logits = torch.from_numpy((rng.standard_normal((len(kinds), vocab)) * 2).astype(np.float32)).to(dtype)
+    params = [_random_params(rng, k) for k in kinds]
+    hist = [rng.integers(0, vocab, int(rng.integers(0, 50))).tolist() for _ in kinds]
+    u = rng.random(len(kinds)).astype(np.float32)
+    rows = sample_rows(logits, hist, params, u)
+    out = run(logits, params, hist, u, probs=True)
+    check(out, rows, params, probs=True, max_boundary_frac=0.2)
+
+
+def test_massive_ties_take_the_row_path():
+    say('ties: constant rows')
+    V = 50000
+    logits = torch.zeros((4, V))
+    params = [SamplingParams(logprobs=3), SamplingParams(temperature=1.0, top_k=5, logprobs=3),
+              SamplingParams(temperature=1.0, top_p=0.5, logprobs=3), SamplingParams(temperature=1.0, logprobs=3)]
+    u = np.float32([0.5, 0.5, 0.5, 0.999])
+    rows = sample_rows(logits, None, params, u)
+    out = run(logits, params, None, u, probs=True)
+    assert int(out.tokens[0]) == 0
+    assert int(out.info['kept'][1]) == V  # every tie with the k-th value survives top-k
+    check(out, rows, params, probs=False, max_boundary_frac=1.0)
+
+
+def test_masked_and_infinite_logits():
+    say('masked logits')
+    V = 3000
+    rng = np.random.default_rng(9)
+    x = (rng.standard_normal((4, V)) * 2).astype(np.float32)
+    x[:, rng.random(V) < 0.7] = -np.inf
+    logits = torch.from_numpy(x)
+    params = [SamplingParams(logprobs=5), SamplingParams(temperature=0.9, top_k=2000, logprobs=5),
+              SamplingParams(temperature=0.9, top_p=0.8, logprobs=5), SamplingParams(temperature=0.9, logprobs=5)]
+    u = rng.random(4).astype(np.float32)
+    rows = sample_rows(logits, None, params, u)
+    out = run(logits, params, None, u, probs=True)
+    check(out, rows, params, probs=True, max_boundary_frac=1.0)
+
+
+def test_strided_and_unaligned_rows():
+    say('strided / unaligned rows')
+    rng = np.random.default_rng(10)
+    V = 20001
+    base = torch.from_numpy((rng.standard_normal((6, V + 7)) * 2).astype(np.float32))
+    params = [SamplingParams(), SamplingParams(temperature=0.7, top_k=20, logprobs=2),
+              SamplingParams(temperature=0.7, top_p=0.9), SamplingParams(temperature=0.7, top_k=3, logprobs=6),
+              SamplingParams(repetition_penalty=1.5, logprobs=2), SamplingParams(temperature=2.0)]
+    hist = [[0, 1, V - 1]] * 6
+    u = rng.random(6).astype(np.float32)
+    strided = base.to(DEV)[:, 3:3 + V]  # row stride V + 7, start offset 3 elements: no 16-byte alignment
+    rows = sample_rows(base[:, 3:3 + V].contiguous(), hist, params, u)
+    out = runner_for(DEV).run(strided, params, hist, u, 6, want_info=True)
+    check(out, rows, params)
+
+
+def test_other_float_dtypes_are_upcast():
+    say('fp16 / fp64 inputs')
+    rng = np.random.default_rng(11)
+    x = torch.from_numpy((rng.standard_normal((2, 5000)) * 2).astype(np.float32))
+    params = [SamplingParams(logprobs=2), SamplingParams(temperature=0.8, top_k=50, logprobs=2)]
+    u = np.float32([0.3, 0.6])
+    for dt in (torch.float16, torch.float64):
+        xs = x.to(dt)
+        rows = sample_rows(xs, None, params, u)
+        out = run(xs, params, None, u)
+        check(out, rows, params)
+
+
+def test_large_top_k_and_top_n():
+    say('large k and N')
+    rng = np.random.default_rng(12)
+    V = 151936
+    x = torch.from_numpy((rng.standard_normal((3, V)) * 2.5).astype(np.float32))
+    params = [SamplingParams(temperature=1.0, top_k=1000, top_p=0.95, logprobs=256),
+              SamplingParams(temperature=1.0, top_k=5000, logprobs=20),
+              SamplingParams(logprobs=256)]
+    u = rng.random(3).astype(np.float32)
+    rows = sample_rows(x, None, params, u)
+    out = run(x, params, None, u)
+    check(out, rows, params)

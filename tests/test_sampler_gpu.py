@@ -1,0 +1,97 @@
+"""The drop-in ``Sampler`` API on the GPU (MI355X only)."""
+import asyncio
+
+import numpy as np
+import pytest
+import torch
+
+from klsample import SampleResult, Sampler, SamplingParams, sample_batch
+from oracle.cpu_sampler import restated_sample
+
+pytestmark = pytest.mark.gpu
+
+
+def test_reference_known_answer_through_the_drop_in():
+    # serving/test_serving.py:101-107, unchanged
+    params = SamplingParams(temperature=.8, top_k=3, top_p=.9, repetition_penalty=1.1,
+                            stop_token_ids=frozenset({2}), seed=7, logprobs=2)
+    logits = torch.tensor([0., 1., 3., 2.])
+    a = Sampler(params).sample(logits, [2])
+    b = Sampler(params).sample(logits, [2])
+    assert a == b and len(a.top_logprobs) == 2
+    assert a.token_id in (2, 3)
+    assert dict(a.top_logprobs)[2] == pytest.approx(-0.33853459, abs=1e-5)
+    assert dict(a.top_logprobs)[3] == pytest.approx(-1.24762559, abs=1e-5)
+    greedy = Sampler(SamplingParams(stop_token_ids=frozenset({2}))).sample(logits)
+    assert greedy.token_id == 2 and greedy.stopped
+
+
+def test_sampler_matches_oracle_with_its_own_uniform():
+    rng = np.random.default_rng(0)
+    x = torch.from_numpy((rng.standard_normal(151936) * 2).astype(np.float32))
+    params = SamplingParams(temperature=0.8, top_k=50, top_p=0.9, seed=123, logprobs=3)
+    s = Sampler(params)
+    gen = torch.Generator().manual_seed(123)
+    for step in range(5):
+        u = float(torch.rand((), generator=gen))
+        want = restated_sample(x, [], params, u=u)
+        got = s.sample(x.cuda())
+        assert got.token_id == want.token_id or want.boundary
+        assert isinstance(got, SampleResult)
+
+
+def test_batching_does_not_change_a_requests_tokens():
+    rng = np.random.default_rng(1)
+    x = torch.from_numpy((rng.standard_normal((6, 32000)) * 2).astype(np.float32)).cuda()
+    params = [SamplingParams(temperature=0.9, top_k=40, top_p=0.95, seed=i, logprobs=2) for i in range(5)]
+    params.append(SamplingParams(repetition_penalty=1.2, logprobs=2))
+    hist = [rng.integers(0, 32000, 30).tolist() for _ in range(6)]
+    single = [Sampler(p) for p in params]
+    batched = [Sampler(p) for p in params]
+    for step in range(3):
+        one = [s.sample(x[i], hist[i]) for i, s in enumerate(single)]
+        many = Sampler.sample_many(batched, x, hist)
+        assert one == many
+
+
+def test_sample_batch_requires_uniforms_for_sampled_rows():
+    x = torch.randn(2, 100).cuda()
+    with pytest.raises(ValueError):
+        sample_batch(x, [SamplingParams(temperature=1.0), SamplingParams()])
+    res = sample_batch(x, [SamplingParams(), SamplingParams()])
+    assert [r.token_id for r in res] == x.argmax(1).tolist()
+
+
+def test_history_errors_mirror_indexing():
+    s = Sampler(SamplingParams(repetition_penalty=1.2))
+    with pytest.raises(IndexError):
+        s.sample(torch.zeros(10), [10])
+    # id -1 is the last token: with r=1.2 its score 9 becomes 7.5, below token 8
+    assert s.sample(torch.arange(10.), [-1]).token_id == 8
+
+
+class _FakeExecutor:
+    """Returns constant host logits per request, like serving/test_serving.py:120-126."""
+
+    async def decode(self, rids):
+        await asyncio.sleep(0)
+        return {r: torch.tensor([0., 1., 3., 2.]) for r in rids}
+
+
+def test_engine_style_loop_runs_unchanged():
+    """The per-row call pattern of serving/engine.py:92-96 and :105-107 with one
+    Sampler per request created at submit time (serving/engine.py:53)."""
+    async def main():
+        samplers = {f'r{i}': Sampler(SamplingParams(stop_token_ids=frozenset({2}))) for i in range(3)}
+        prompts = {r: (5, 6, 7) for r in samplers}
+        generated = {r: [] for r in samplers}
+        first = {r: samplers[r].sample(torch.tensor([0., 1., 3., 2.]), prompts[r]) for r in samplers}
+        for r, res in first.items():
+            generated[r].append(res.token_id)
+        logits = await _FakeExecutor().decode(list(samplers))
+        for r in samplers:
+            res = samplers[r].sample(logits[r], prompts[r] + tuple(generated[r]))
+            generated[r].append(res.token_id)
+            assert res.stopped
+        return generated
+    assert asyncio.run(main()) == {f'r{i}': [2, 2] for i in range(3)}
