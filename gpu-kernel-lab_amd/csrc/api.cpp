@@ -3,6 +3,7 @@
 #include <stdarg.h>
 #include <stdint.h>
 #include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include <string>
@@ -64,6 +65,12 @@ bool make_plan(int32_t batch, int32_t vocab, int32_t dtype, int32_t max_top_k, i
         const int64_t s = (vocab + chunk - 1) / chunk;
         if ((int64_t)batch * s >= 2048) { e = cands[i]; break; }
     }
+    // KLSAMPLE_ELEMS_PER_THREAD pins E (tuning); ignored unless it names a built variant
+    if (const char *env = getenv("KLSAMPLE_ELEMS_PER_THREAD")) {
+        const int want = atoi(env);
+        for (int i = 0; i < ncands; ++i)
+            if (cands[i] == want) e = want;
+    }
     p->elems = e;
     p->chunk = kThreads * e;
     p->chunks = (vocab + p->chunk - 1) / p->chunk;
@@ -75,8 +82,7 @@ bool make_plan(int32_t batch, int32_t vocab, int32_t dtype, int32_t max_top_k, i
     p->cand_cap = (int32_t)cap;
     const size_t B = (size_t)batch, S = (size_t)p->chunks;
     size_t off = 0;
-    // tickets first and sized for the largest batch, so every plan finds them zero
-    p->off_tickets = off; off = align_up(off + (size_t)kMaxBatch * sizeof(uint32_t), 256);
+    p->off_count = off;   off = align_up(off + B * sizeof(uint32_t), 256);
     p->off_stats = off;   off = align_up(off + B * S * sizeof(ChunkStat), 256);
     p->off_cands = off;   off = align_up(off + B * S * (size_t)cap * sizeof(Cand), 256);
     p->off_rows = off;    off = align_up(off + B * sizeof(klsample_row_info), 256);
@@ -128,7 +134,7 @@ int klsample_run(const klsample_batch *b, void *stream) {
         return fail(KLSAMPLE_ERR_INVALID_ARGUMENT, "top_ids and top_logprobs are required when num_logprobs > 0");
     if (b->history_offsets != nullptr && b->history_ids == nullptr)
         return fail(KLSAMPLE_ERR_INVALID_ARGUMENT, "history_ids must not be NULL when history_offsets is given");
-    if ((b->options & ~(uint32_t)(KLSAMPLE_OPT_FORCE_DENSE | KLSAMPLE_OPT_SPLIT_COMBINE)) != 0)
+    if ((b->options & ~(uint32_t)KLSAMPLE_OPT_FORCE_DENSE) != 0)
         return fail(KLSAMPLE_ERR_INVALID_ARGUMENT, "unknown option bits 0x%x", b->options);
     if (b->workspace == nullptr) return fail(KLSAMPLE_ERR_WORKSPACE, "workspace must not be NULL");
     if (((uintptr_t)b->workspace & 255u) != 0) return fail(KLSAMPLE_ERR_WORKSPACE, "workspace must be 256-byte aligned");
@@ -157,7 +163,7 @@ int klsample_run(const klsample_batch *b, void *stream) {
     a.probs = b->probs;
     a.row_info = b->row_info;
     unsigned char *ws = static_cast<unsigned char *>(b->workspace);
-    a.tickets = reinterpret_cast<uint32_t *>(ws + plan.off_tickets);
+    a.cand_count = reinterpret_cast<uint32_t *>(ws + plan.off_count);
     a.stats = reinterpret_cast<kls::ChunkStat *>(ws + plan.off_stats);
     a.cands = reinterpret_cast<kls::Cand *>(ws + plan.off_cands);
     a.rows = reinterpret_cast<klsample_row_info *>(ws + plan.off_rows);
@@ -166,6 +172,7 @@ int klsample_run(const klsample_batch *b, void *stream) {
     a.C = plan.chunk;
     a.S = plan.chunks;
     a.cand_cap = plan.cand_cap;
+    a.row_cap = plan.cand_cap * plan.chunks;
     a.vec_ok = (((uintptr_t)b->logits & 15u) == 0 && ((size_t)b->row_stride * esize) % 16 == 0) ? 1 : 0;
     a.xcd_map = (b->batch % 8 == 0) ? 1 : 0;
 

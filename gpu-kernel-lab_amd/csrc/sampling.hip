@@ -11,17 +11,19 @@
 //                   shuffles, and writes the chunk's candidates: every element at or
 //                   above a lower bound on the chunk's K-th largest value, found by a
 //                   one-wave bisection over the keys of per-thread group maxima.
-//                   The last workgroup of a row to finish (atomic ticket) combines
-//                   the row.
-//   combine_row     sorts the row's candidates in LDS (bitonic, <= 2048), applies
-//                   top-k / top-p exactly on them, draws by inverse CDF in vocab
-//                   order, and writes token, logprob and top-N.  Rows the candidates
-//                   cannot settle (top-p mass beyond the candidates, slot overflow on
-//                   massive ties) are marked for dense_kernel.
-//   dense_kernel    one workgroup per row; rows not marked exit at once.  A marked
-//                   row is resolved by radix selects over the whole row (count- and
-//                   mass-weighted, 8-bit digits, LDS histograms).
+//   row_kernel      one workgroup per row.  combine_row gathers the row's candidates
+//                   (flattened over chunks), sorts them in LDS (bitonic, <= 2048),
+//                   applies top-k / top-p exactly on them, draws by inverse CDF in
+//                   vocab order, and writes token, logprob and top-N.  Rows the
+//                   candidates cannot settle (top-p mass beyond the candidates, slot
+//                   overflow on massive ties) take dense_resolve: radix selects over
+//                   the whole row (count- and mass-weighted, 8-bit digits, LDS
+//                   histograms).
 //   probs_kernel    optional: the final probability vector of each row.
+//
+// The two main launches are separate kernels on purpose: handing a row to the last
+// chunk workgroup would need a device-scope release per workgroup, which on gfx950 is
+// an L2 writeback plus invalidate and costs more than the second launch.
 //
 // There is no dense contraction anywhere, so no MFMA: the streaming pass is bound by
 // HBM bandwidth (bytes per row = V * sizeof(logit) + 4 * H).
@@ -37,7 +39,6 @@ namespace {
 
 constexpr float kNegInf = -__builtin_huge_valf();
 constexpr double kFixScale = 1099511627776.0;  // 2^40: fixed-point unit of the row path's masses
-constexpr int kPathPending = -1;               // row state: waiting for dense_kernel
 
 __device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
 __device__ __forceinline__ int wave_id() { return threadIdx.x >> 6; }
@@ -112,10 +113,74 @@ struct Misc {
     double da, db;
 };
 
+// ---------------------------------------------------------------------------------
+// Wave64 primitives on DPP (no LDS round trip): quad_perm / row mirrors / row_bcast
+// reduce a wave in six steps; row_shr + row_bcast give an inclusive scan and
+// wave_shr:1 turns it exclusive.  Values wider than 32 bits move as two halves.
+template <typename To, typename From>
+__device__ __forceinline__ To bitcast(From v) { return __builtin_bit_cast(To, v); }
+
+template <int CTRL, int ROW_MASK = 0xf, int BANK_MASK = 0xf>
+__device__ __forceinline__ uint32_t dpp32(uint32_t old, uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_update_dpp((int)old, (int)v, CTRL, ROW_MASK, BANK_MASK, false);
+}
+
+template <int CTRL, int ROW_MASK = 0xf, int BANK_MASK = 0xf, typename T>
+__device__ __forceinline__ T dpp(T old, T v) {
+    if constexpr (sizeof(T) == 4) {
+        return bitcast<T>(dpp32<CTRL, ROW_MASK, BANK_MASK>(bitcast<uint32_t>(old), bitcast<uint32_t>(v)));
+    } else {
+        const uint64_t o = bitcast<uint64_t>(old), x = bitcast<uint64_t>(v);
+        const uint32_t lo = dpp32<CTRL, ROW_MASK, BANK_MASK>((uint32_t)o, (uint32_t)x);
+        const uint32_t hi = dpp32<CTRL, ROW_MASK, BANK_MASK>((uint32_t)(o >> 32), (uint32_t)(x >> 32));
+        return bitcast<T>(((uint64_t)hi << 32) | lo);
+    }
+}
+
+template <typename T>
+__device__ __forceinline__ T readlane(T v, int lane) {
+    if constexpr (sizeof(T) == 4) {
+        return bitcast<T>((uint32_t)__builtin_amdgcn_readlane((int)bitcast<uint32_t>(v), lane));
+    } else {
+        const uint64_t x = bitcast<uint64_t>(v);
+        const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)x, lane);
+        const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(x >> 32), lane);
+        return bitcast<T>(((uint64_t)hi << 32) | lo);
+    }
+}
+
+// Reduction over the 64 lanes of a fully active wave; the result is wave-uniform.
 template <typename T, typename Op>
-__device__ T block_reduce(T v, Op op, T *scratch) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = op(v, __shfl_xor(v, o, 64));
+__device__ __forceinline__ T wave_reduce(T v, Op op, T id) {
+    v = op(v, dpp<0xb1>(id, v));         // quad_perm [1,0,3,2]
+    v = op(v, dpp<0x4e>(id, v));         // quad_perm [2,3,0,1]
+    v = op(v, dpp<0x141>(id, v));        // row_half_mirror
+    v = op(v, dpp<0x140>(id, v));        // row_mirror
+    v = op(v, dpp<0x142, 0xa>(id, v));   // row_bcast:15 into rows 1 and 3
+    v = op(v, dpp<0x143, 0xc>(id, v));   // row_bcast:31 into rows 2 and 3
+    return readlane(v, 63);
+}
+
+// Inclusive prefix sum over the lanes of a fully active wave.
+template <typename T>
+__device__ __forceinline__ T wave_incl_scan(T v) {
+    const T z = T(0);
+    v = v + dpp<0x111>(z, v);            // row_shr:1
+    v = v + dpp<0x112>(z, v);            // row_shr:2
+    v = v + dpp<0x114>(z, v);            // row_shr:4
+    v = v + dpp<0x118>(z, v);            // row_shr:8
+    v = v + dpp<0x142, 0xa>(z, v);       // row_bcast:15
+    v = v + dpp<0x143, 0xc>(z, v);       // row_bcast:31
+    return v;
+}
+
+// Exclusive form of an inclusive lane scan (lane 0 gets 0).
+template <typename T>
+__device__ __forceinline__ T wave_shift_excl(T incl) { return dpp<0x138>(T(0), incl); }  // wave_shr:1
+
+template <typename T, typename Op>
+__device__ T block_reduce(T v, Op op, T *scratch, T id) {
+    v = wave_reduce(v, op, id);
     __syncthreads();
     if (lane_id() == 0) scratch[wave_id()] = v;
     __syncthreads();
@@ -135,35 +200,30 @@ struct OpSumQ {
 };
 struct OpOrI { __device__ int operator()(int a, int b) const { return a | b; } };
 
-__device__ __forceinline__ float block_max(float v, Misc &ms) { return block_reduce(v, OpMaxF(), ms.red.f); }
-__device__ __forceinline__ int block_min(int v, Misc &ms) { return block_reduce(v, OpMinI(), ms.red.i); }
-__device__ __forceinline__ int block_maxi(int v, Misc &ms) { return block_reduce(v, OpMaxI(), ms.red.i); }
-__device__ __forceinline__ int block_sum(int v, Misc &ms) { return block_reduce(v, OpSumI(), ms.red.i); }
-__device__ __forceinline__ double block_sumd(double v, Misc &ms) { return block_reduce(v, OpSumD(), ms.red.d); }
+__device__ __forceinline__ float block_max(float v, Misc &ms) { return block_reduce(v, OpMaxF(), ms.red.f, kNegInf); }
+__device__ __forceinline__ int block_min(int v, Misc &ms) { return block_reduce(v, OpMinI(), ms.red.i, 0x7fffffff); }
+__device__ __forceinline__ int block_maxi(int v, Misc &ms) { return block_reduce(v, OpMaxI(), ms.red.i, (int)0x80000000); }
+__device__ __forceinline__ int block_sum(int v, Misc &ms) { return block_reduce(v, OpSumI(), ms.red.i, 0); }
+__device__ __forceinline__ int block_or(int v, Misc &ms) { return block_reduce(v, OpOrI(), ms.red.i, 0); }
+__device__ __forceinline__ double block_sumd(double v, Misc &ms) { return block_reduce(v, OpSumD(), ms.red.d, 0.0); }
 __device__ __forceinline__ unsigned long long block_sumq(unsigned long long v, Misc &ms) {
-    return block_reduce(v, OpSumQ(), ms.red.q);
+    return block_reduce(v, OpSumQ(), ms.red.q, 0ull);
 }
 
 // Exclusive scan over the workgroup in thread order; `total` receives the sum.
 template <typename T>
 __device__ T block_excl_scan(T v, T *scratch, T &total) {
-    const int lane = lane_id(), wave = wave_id();
-    T incl = v;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        T y = __shfl_up(incl, o, 64);
-        if (lane >= o) incl += y;
-    }
-    T excl = __shfl_up(incl, 1, 64);
-    if (lane == 0) excl = T(0);
+    const T incl = wave_incl_scan(v);
+    const T excl = wave_shift_excl(incl);
+    const T wt = readlane(incl, 63);
     __syncthreads();
-    if (lane == 63) scratch[wave] = incl;
+    if (lane_id() == 0) scratch[wave_id()] = wt;
     __syncthreads();
     T base = T(0), tot = T(0);
 #pragma unroll
     for (int w = 0; w < kWaves; ++w) {
         const T s = scratch[w];
-        if (w < wave) base += s;
+        if (w < wave_id()) base += s;
         tot += s;
     }
     total = tot;
@@ -231,6 +291,7 @@ template <int E, int G>
 __device__ float group_bound(const float (&x)[E], int K, uint32_t *keys, Misc &ms) {
     constexpr int GS = E / G;
     constexpr int NG = kThreads * G;
+    constexpr int PER = NG / 64;   // keys per lane of the counting wave
 #pragma unroll
     for (int g = 0; g < G; ++g) {
         float mx = kNegInf;
@@ -240,29 +301,45 @@ __device__ float group_bound(const float (&x)[E], int K, uint32_t *keys, Misc &m
     }
     __syncthreads();
     if (wave_id() == 0) {
+        // largest t with #{keys >= t} >= K, bit by bit from the top; counts are wave
+        // ballots, so each step is a compare and a scalar popcount per key slot
         const int lane = lane_id();
         uint32_t t = 0u;
-        for (int bit = 31; bit >= 0; --bit) {
-            const uint32_t cand = t | (1u << bit);
-            int c = 0;
-#pragma unroll 4
-            for (int j = lane; j < NG; j += 64) c += (keys[j] >= cand) ? 1 : 0;
+        if constexpr (PER <= 4) {
+            uint32_t k[PER];
 #pragma unroll
-            for (int o = 32; o > 0; o >>= 1) c += __shfl_xor(c, o, 64);
-            if (c >= K) t = cand;
+            for (int j = 0; j < PER; ++j) k[j] = keys[j * 64 + lane];
+            // the low 8 key bits stay zero: the bound sits at most 2^-15 (relative)
+            // below the exact K-th group maximum, a handful of extra candidates
+            for (int bit = 31; bit >= 8; --bit) {
+                const uint32_t cand = t | (1u << bit);
+                int c = 0;
+#pragma unroll
+                for (int j = 0; j < PER; ++j) c += __popcll(__ballot(k[j] >= cand));
+                if (c >= K) t = cand;
+            }
+        } else {
+            // many keys per lane: re-read them from LDS every step (volatile keeps the
+            // compiler from hoisting all of them into registers for the whole kernel)
+            const volatile uint32_t *vk = keys;
+#pragma unroll 1
+            for (int bit = 31; bit >= 8; --bit) {
+                const uint32_t cand = t | (1u << bit);
+                int c = 0;
+#pragma unroll 4
+                for (int j = 0; j < PER; ++j) c += __popcll(__ballot(vk[j * 64 + lane] >= cand));
+                if (c >= K) t = cand;
+            }
         }
         if (lane == 0) ms.bound_key = t;
     }
     __syncthreads();
-    return fkey_inv(ms.bound_key);
+    // keys below that of -FLT_MAX stand for -inf (groups without a finite element)
+    return ms.bound_key < 0x00800000u ? kNegInf : fkey_inv(ms.bound_key);
 }
 
 template <int E>
-__device__ float chunk_bound(const float (&x)[E], int K, uint32_t *keys, Misc &ms) {
-    // smallest G with kThreads*G >= 4K (tight bound), capped by E and kMaxGroupKeys
-    int G = 1;
-    while (G < E && G * kThreads < kMaxGroupKeys && G * kThreads < 4 * K) G <<= 1;
-    if (K > G * kThreads) return kNegInf;   // fewer groups than K: no bound, keep all
+__device__ float group_bound_dispatch(const float (&x)[E], int G, int K, uint32_t *keys, Misc &ms) {
     switch (G) {
         case 1: return group_bound<E, 1>(x, K, keys, ms);
         case 2: if constexpr (E >= 2) return group_bound<E, 2>(x, K, keys, ms); break;
@@ -273,25 +350,49 @@ __device__ float chunk_bound(const float (&x)[E], int K, uint32_t *keys, Misc &m
     return kNegInf;
 }
 
+// Lower bound on the chunk's K-th largest element (-inf: keep every element).  Groups
+// start as coarse as 4K groups allow and are refined while fewer than K of them hold a
+// finite element (a partial last chunk, masked logits).
+template <int E>
+__device__ float chunk_bound(const float (&x)[E], int K, uint32_t *keys, Misc &ms) {
+    constexpr int kMaxG = (E < kMaxGroupKeys / kThreads) ? E : kMaxGroupKeys / kThreads;
+    int G = 1;
+    while (G < kMaxG && G * kThreads < 4 * K) G <<= 1;
+    if (K > G * kThreads) return kNegInf;
+    float bound = group_bound_dispatch<E>(x, G, K, keys, ms);
+    while (bound == kNegInf && G < kMaxG) {
+        G <<= 1;
+        bound = group_bound_dispatch<E>(x, G, K, keys, ms);
+    }
+    return bound;
+}
+
 // ---------------------------------------------------------------------------------
 // Radix selection over a row's entries.  A source enumerates (key, index, score)
 // for the entries it contains; each thread visits a disjoint subset.
 
+// The row's candidates: one contiguous list, read four entries per thread at a time.
 struct CandSource {
     const Cand *cands;
-    const ChunkStat *st;
-    int S, cap;
+    int n;
     float lo;
     template <class F>
+    __device__ __forceinline__ void visit(uint2 e, F &f) const {
+        const float y = __uint_as_float(e.x);
+        if (y >= lo) f(fkey(y), (int)e.y, y);
+    }
+    template <class F>
     __device__ void each(F f) const {
-        for (int c = 0; c < S; ++c) {
-            const int n = min(st[c].ncand, cap);
-            const Cand *p = cands + (size_t)c * cap;
-            for (int j = threadIdx.x; j < n; j += kThreads) {
-                const Cand e = p[j];
-                if (e.y >= lo) f(fkey(e.y), e.idx, e.y);
-            }
+        const uint2 *p = reinterpret_cast<const uint2 *>(cands);
+        int t = threadIdx.x;
+        for (; t + 3 * kThreads < n; t += 4 * kThreads) {
+            const uint2 e0 = p[t], e1 = p[t + kThreads], e2 = p[t + 2 * kThreads], e3 = p[t + 3 * kThreads];
+            visit(e0, f);
+            visit(e1, f);
+            visit(e2, f);
+            visit(e3, f);
         }
+        for (; t < n; t += kThreads) visit(p[t], f);
     }
 };
 
@@ -320,12 +421,7 @@ __device__ void pick_digit_count(Misc &ms, uint32_t need) {
         uint32_t c[4], s = 0;
 #pragma unroll
         for (int j = 0; j < 4; ++j) { c[j] = ms.hist[255 - 4 * l - j]; s += c[j]; }
-        uint32_t incl = s;
-#pragma unroll
-        for (int o = 1; o < 64; o <<= 1) {
-            const uint32_t y = __shfl_up(incl, o, 64);
-            if (l >= o) incl += y;
-        }
+        const uint32_t incl = wave_incl_scan(s);
         const uint32_t excl = incl - s;
         const unsigned long long bal = __ballot(incl >= need);
         const int first = bal ? (__ffsll((long long)bal) - 1) : 63;
@@ -403,14 +499,8 @@ __device__ bool select_mass(const Src &src, double target, double m, MassPick &o
                 c[j] = ms.hmass[255 - 4 * l - j]; s += c[j];
                 n[j] = ms.hist[255 - 4 * l - j]; ns += n[j];
             }
-            unsigned long long incl = s;
-            uint32_t nincl = ns;
-#pragma unroll
-            for (int o = 1; o < 64; o <<= 1) {
-                const unsigned long long y = __shfl_up(incl, o, 64);
-                const uint32_t ny = __shfl_up(nincl, o, 64);
-                if (l >= o) { incl += y; nincl += ny; }
-            }
+            const unsigned long long incl = wave_incl_scan(s);
+            const uint32_t nincl = wave_incl_scan(ns);
             const unsigned long long bal = __ballot((double)(above + incl) > target);
             if (bal == 0ull) {
                 if (l == 0) ms.sel_found = 0;
@@ -694,14 +784,16 @@ __device__ void dense_resolve(const Args &a, int row, const klsample_row_params 
     int count = 0;
     if (mode == kGreedy) {
         unsigned long long zq = 0ull;
-        all.each([&](uint32_t, int, float y) { zq += wfix(y); });
+        int nfin = 0;
+        all.each([&](uint32_t, int, float y) { zq += wfix(y); nfin += (y > kNegInf) ? 1 : 0; });
         zq = block_sumq(zq, ms);
+        nfin = block_sum(nfin, ms);
         r.token = arg;
         r.log_norm = log((double)zq / kFixScale);
         r.logprob = -r.log_norm;
         r.cut = kNegInf;
         r.cut_idx = V;
-        r.kept = V;
+        r.kept = nfin;
         count = dense_topn(all, a.N, sortbuf, ms);
     } else {
         float lo = kNegInf;
@@ -709,7 +801,7 @@ __device__ void dense_resolve(const Args &a, int row, const klsample_row_params 
         const DenseSource ge{yb, V, lo, V};
         unsigned long long zk = 0ull;
         int nk = 0;
-        ge.each([&](uint32_t, int, float y) { zk += wfix(y); ++nk; });
+        ge.each([&](uint32_t, int, float y) { zk += wfix(y); nk += (y > kNegInf) ? 1 : 0; });
         zk = block_sumq(zk, ms);
         nk = block_sum(nk, ms);
         float cut = lo;
@@ -760,29 +852,29 @@ __device__ void dense_resolve(const Args &a, int row, const klsample_row_params 
 // Resolve one row from its chunk summaries and candidates (or hand it to
 // dense_resolve).  Runs in one workgroup of kThreads.
 // Resolve one row from its chunk summaries and candidates.  Runs in one workgroup
-// of kThreads.  Returns false when the candidates cannot settle the row; the row is
-// then marked for dense_kernel.
+// of kThreads.  Returns false when the candidates cannot settle the row (the caller
+// then runs dense_resolve).
 template <typename TIn, int E>
 __device__ bool combine_row(const Args &a, int row, const klsample_row_params &p, int mode,
                             unsigned char *raw, Misc &ms) {
     constexpr int C = kThreads * E;
     const int S = a.S, V = a.V, N = a.N;
+    if (a.options & KLSAMPLE_OPT_FORCE_DENSE) return false;
     const ChunkStat *st = a.stats + (size_t)row * S;
-    const Cand *cands = a.cands + (size_t)row * S * a.cand_cap;
+    const uint32_t listed = a.cand_count[row];
+    if (listed > (uint32_t)a.row_cap) return false;   // candidate list overflowed (massive ties)
 
     float m = kNegInf, lo = kNegInf;
-    int ovf = 0;
+    int arg = 0x7fffffff, nfinite = 0;
     for (int c = threadIdx.x; c < S; c += kThreads) {
         const ChunkStat s = st[c];
         m = fmaxf(m, s.m);
         lo = fmaxf(lo, s.y_thr);
-        ovf |= s.overflow;
+        nfinite += s.nfinite;
     }
     m = block_max(m, ms);
     lo = block_max(lo, ms);
-    ovf = block_reduce(ovf, OpOrI(), ms.red.i);
-    if (ovf || (a.options & KLSAMPLE_OPT_FORCE_DENSE)) { return false; }
-    int arg = 0x7fffffff;
+    nfinite = block_sum(nfinite, ms);
     double Z = 0.0;
     for (int c = threadIdx.x; c < S; c += kThreads) {
         const ChunkStat s = st[c];
@@ -793,7 +885,7 @@ __device__ bool combine_row(const Args &a, int row, const klsample_row_params &p
     Z = block_sumd(Z, ms);
 
     // candidate set F = { y >= lo }: complete above lo
-    CandSource src{cands, st, S, a.cand_cap, lo};
+    CandSource src{a.cands + (size_t)row * a.row_cap, (int)listed, lo};
     int nF = 0;
     src.each([&](uint32_t, int, float) { ++nF; });
     nF = block_sum(nF, ms);
@@ -832,7 +924,7 @@ __device__ bool combine_row(const Args &a, int row, const klsample_row_params &p
         r.m = m;
         r.cut = kNegInf;
         r.cut_idx = V;
-        r.kept = V;
+        r.kept = nfinite;
         r.log_norm = log(Z);
         if (mode == kGreedy) {
             r.token = (arg == 0x7fffffff) ? 0 : arg;
@@ -958,7 +1050,7 @@ __device__ __forceinline__ void map_block(const Args &a, int &row, int &chunk) {
     const int w = blockIdx.x;
     if (a.xcd_map) {
         // consecutive workgroup ids go to consecutive XCDs: keep a row's chunks on one
-        // XCD so the row's history and candidates stay in one L2
+        // XCD so the row's history is fetched into one L2
         const int xcd = w & 7, slot = w >> 3;
         row = xcd + 8 * (slot / a.S);
         chunk = slot % a.S;
@@ -969,21 +1061,27 @@ __device__ __forceinline__ void map_block(const Args &a, int &row, int &chunk) {
 }
 
 template <int C>
-struct RawBytes {
+struct ScanLds {
     static constexpr int a = C * 4;
-    static constexpr int b = kSortCap * 8;
-    static constexpr int c = kMaxGroupKeys * 4;
-    static constexpr int ab = a > b ? a : b;
-    static constexpr int value = ab > c ? ab : c;
+    static constexpr int b = kMaxGroupKeys * 4;
+    static constexpr int value = a > b ? a : b;
 };
 
-// Streaming pass: one workgroup per (row, chunk).
+template <int C>
+struct RowLds {
+    static constexpr int a = C * 4;
+    static constexpr int b = kSortCap * 8;
+    static constexpr int value = a > b ? a : b;
+};
+
+// Streaming pass: one workgroup per (row, chunk).  At least four waves per SIMD must
+// fit: that is what the LDS footprint of the largest chunk allows anyway.
 template <typename TIn, int E>
-__global__ __launch_bounds__(kThreads) void scan_kernel(Args a) {
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) void scan_kernel(Args a) {
     constexpr int VW = Loader<TIn>::VW;
     constexpr int NV = E / VW;
     constexpr int C = kThreads * E;
-    __shared__ __attribute__((aligned(16))) unsigned char raw[RawBytes<C>::value];
+    __shared__ __attribute__((aligned(16))) unsigned char raw[ScanLds<C>::value];
     __shared__ Misc ms;
 
     int row, chunk;
@@ -998,14 +1096,18 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(Args a) {
     if (tid == 0) ms.ncand = 0;
 
     float x[E];
+    if (cn == C && a.vec_ok) {
+        // full chunk: every 16-byte load issued back to back
 #pragma unroll
-    for (int v = 0; v < NV; ++v) {
-        const int li = (v * kThreads + tid) * VW;
-        if (a.vec_ok && li + VW <= cn) {
-            Loader<TIn>::vec(src + li, &x[v * VW]);
-        } else {
+        for (int v = 0; v < NV; ++v) Loader<TIn>::vec(src + (v * kThreads + tid) * VW, &x[v * VW]);
+    } else {
 #pragma unroll
-            for (int e = 0; e < VW; ++e) x[v * VW + e] = (li + e < cn) ? Loader<TIn>::one(src + li + e) : kNegInf;
+        for (int v = 0; v < NV; ++v) {
+#pragma unroll
+            for (int e = 0; e < VW; ++e) {
+                const int li = (v * kThreads + tid) * VW + e;
+                x[v * VW + e] = (li < cn) ? Loader<TIn>::one(src + li) : kNegInf;
+            }
         }
     }
 
@@ -1035,7 +1137,7 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(Args a) {
     st.ncand = 0;
     st.z = 0.0;
     st.overflow = 0;
-    st.pad = 0;
+    st.nfinite = 0;
     if (mode != kTopK) {
         float mt = kNegInf;
 #pragma unroll
@@ -1054,11 +1156,16 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(Args a) {
             st.arg = (at == 0x7fffffff) ? 0x7fffffff : c0 + at;
         }
         double z = 0.0;
+        int nfin = 0;
         if (m > kNegInf) {
 #pragma unroll
-            for (int e = 0; e < E; ++e) z += (double)exp_fast(x[e] - m);
+            for (int e = 0; e < E; ++e) {
+                z += (double)exp_fast(x[e] - m);
+                nfin += (x[e] > kNegInf) ? 1 : 0;
+            }
         }
         st.z = block_sumd(z, ms);
+        st.nfinite = block_sum(nfin, ms);
         st.m = m;
     }
 
@@ -1079,18 +1186,17 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(Args a) {
         int my = 0;
 #pragma unroll
         for (int e = 0; e < E; ++e) my += (x[e] >= thr && x[e] > kNegInf) ? 1 : 0;
-        int incl = my;
-#pragma unroll
-        for (int o = 1; o < 64; o <<= 1) {
-            const int y = __shfl_up(incl, o, 64);
-            if (lane_id() >= o) incl += y;
-        }
-        const int wtot = __shfl(incl, 63, 64);
+        const int incl = wave_incl_scan(my);
+        const int wtot = readlane(incl, 63);
         int wbase = 0;
-        if (lane_id() == 63 && wtot > 0) wbase = atomicAdd(&ms.ncand, wtot);
-        wbase = __shfl(wbase, 63, 64);
-        int pos = wbase + incl - my;
-        Cand *out = a.cands + ((size_t)row * a.S + chunk) * a.cand_cap;
+        if (lane_id() == 0 && wtot > 0) wbase = atomicAdd(&ms.ncand, wtot);
+        wbase = readlane(wbase, 0);
+        __syncthreads();
+        // one append per workgroup to the row's contiguous candidate list
+        if (tid == 0) ms.ia = ms.ncand > 0 ? (int)atomicAdd(&a.cand_count[row], (uint32_t)ms.ncand) : 0;
+        __syncthreads();
+        int pos = ms.ia + wbase + incl - my;
+        Cand *out = a.cands + (size_t)row * a.row_cap;
 #pragma unroll
         for (int v = 0; v < NV; ++v) {
             const int li = (v * kThreads + tid) * VW;
@@ -1098,7 +1204,7 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(Args a) {
             for (int e = 0; e < VW; ++e) {
                 const float xv = x[v * VW + e];
                 if (xv >= thr && xv > kNegInf) {
-                    if (pos < a.cand_cap) {
+                    if (pos < a.row_cap) {
                         Cand cd;
                         cd.y = (mode == kTopK) ? __fdiv_rn(xv, p.temperature) : xv;
                         cd.idx = c0 + li + e;
@@ -1108,49 +1214,23 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(Args a) {
                 }
             }
         }
-        __syncthreads();
-        const int total = ms.ncand;
-        st.ncand = min(total, a.cand_cap);
-        st.overflow = total > a.cand_cap ? 1 : 0;
+        st.ncand = ms.ncand;
     }
     if (tid == 0) a.stats[(size_t)row * a.S + chunk] = st;
-    if (a.options & KLSAMPLE_OPT_SPLIT_COMBINE) return;
-
-    // the last workgroup of the row to finish combines it
-    __syncthreads();
-    if (tid == 0) {
-        __threadfence();
-        const uint32_t t = atomicAdd(&a.tickets[row], 1u);
-        ms.last = (t == (uint32_t)a.S - 1u) ? 1 : 0;
-    }
-    __syncthreads();
-    if (!ms.last) return;
-    __threadfence();
-    if (tid == 0) a.tickets[row] = 0u;
-    if (!combine_row<TIn, E>(a, row, p, mode, raw, ms) && tid == 0) a.rows[row].path = kPathPending;
 }
 
+// One workgroup per row: combine the chunk candidates, or run the multi-pass path.
 template <typename TIn, int E>
-__global__ __launch_bounds__(kThreads) void combine_kernel(Args a) {
+__global__ __launch_bounds__(kThreads) void row_kernel(Args a) {
     constexpr int C = kThreads * E;
-    __shared__ __attribute__((aligned(16))) unsigned char raw[RawBytes<C>::value];
+    __shared__ __attribute__((aligned(16))) unsigned char raw[RowLds<C>::value];
     __shared__ Misc ms;
     const int row = blockIdx.x;
     const klsample_row_params p = a.params[row];
-    if (!combine_row<TIn, E>(a, row, p, row_mode(p, a.V), raw, ms) && threadIdx.x == 0)
-        a.rows[row].path = kPathPending;
-}
-
-// Multi-pass path for the rows combine_row marked; every other workgroup exits at once.
-template <typename TIn, int E>
-__global__ __launch_bounds__(kThreads) void dense_kernel(Args a) {
-    constexpr int C = kThreads * E;
-    __shared__ __attribute__((aligned(16))) unsigned char raw[RawBytes<C>::value];
-    __shared__ Misc ms;
-    const int row = blockIdx.x;
-    if (a.rows[row].path != kPathPending) return;
-    const klsample_row_params p = a.params[row];
-    dense_resolve<TIn, E>(a, row, p, row_mode(p, a.V), raw, ms);
+    const int mode = row_mode(p, a.V);
+    if (!combine_row<TIn, E>(a, row, p, mode, raw, ms)) dense_resolve<TIn, E>(a, row, p, mode, raw, ms);
+    // leave the row's candidate list empty for the next call (read once, at the start)
+    if (threadIdx.x == 0) a.cand_count[row] = 0u;
 }
 
 // Final probabilities: exp(s - max - log_norm) on the kept set, 0 elsewhere.
@@ -1188,8 +1268,7 @@ template <typename TIn, int E>
 hipError_t launch_typed(const Args &a, hipStream_t s) {
     const dim3 grid((unsigned)((int64_t)a.B * a.S));
     scan_kernel<TIn, E><<<grid, kThreads, 0, s>>>(a);
-    if (a.options & KLSAMPLE_OPT_SPLIT_COMBINE) combine_kernel<TIn, E><<<dim3((unsigned)a.B), kThreads, 0, s>>>(a);
-    dense_kernel<TIn, E><<<dim3((unsigned)a.B), kThreads, 0, s>>>(a);
+    row_kernel<TIn, E><<<dim3((unsigned)a.B), kThreads, 0, s>>>(a);
     if (a.probs) probs_kernel<TIn, E><<<grid, kThreads, 0, s>>>(a);
     return hipGetLastError();
 }

@@ -29,7 +29,6 @@ ROW_PRESENCE_FREQUENCY = 4
 ROW_TOP_P = 8
 
 OPT_FORCE_DENSE = 1
-OPT_SPLIT_COMBINE = 2
 
 MAX_LOGPROBS = 256
 MAX_BATCH = 65536

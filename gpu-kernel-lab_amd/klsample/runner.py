@@ -153,9 +153,11 @@ class DeviceRunner:
             raise ValueError('logits must be [batch, vocab]')
         if logits.dtype not in _DTYPES:
             logits = logits.float()
-        if logits.stride(1) != 1:
-            logits = logits.contiguous()
         B, V = logits.shape
+        # rows must not overlap (a size-1 dimension may carry any stride)
+        if logits.stride(1) != 1 or (B > 1 and logits.stride(0) < V):
+            logits = logits.contiguous()
+        row_stride = logits.stride(0) if B > 1 else V
         N = int(num_logprobs)
         rows, offsets, ids, max_top_k = pack_rows(params_list, histories, uniforms, V)
         stream = torch.cuda.current_stream(self.device)
@@ -191,7 +193,7 @@ class DeviceRunner:
 
         batch = _lib.Batch()
         batch.logits = logits.data_ptr()
-        batch.row_stride = logits.stride(0)
+        batch.row_stride = row_stride
         batch.dtype = _DTYPES[logits.dtype]
         batch.batch = B
         batch.vocab = V

@@ -49,7 +49,6 @@ extern "C" {
 
 /* klsample_batch.options */
 #define KLSAMPLE_OPT_FORCE_DENSE 1u       /* resolve every row on the multi-pass path (testing) */
-#define KLSAMPLE_OPT_SPLIT_COMBINE 2u     /* combine rows in a second launch instead of the last chunk */
 
 /* Per-row sampling parameters (32 bytes).  Mirrors SamplingParams
  * (serving/sampling.py:8-15) plus presence/frequency and the row's uniform.
@@ -112,7 +111,7 @@ int klsample_workspace_size(int32_t batch, int32_t vocab, int32_t dtype, int32_t
                             int32_t num_logprobs, size_t *bytes);
 
 /* Zero-fill a workspace before its first use (enqueued on `stream`, a hipStream_t).
- * Calls leave the workspace in the state they found it, so this is needed once per
+ * A call leaves the workspace ready for the next one, so this is needed once per
  * allocation. */
 int klsample_workspace_init(void *workspace, size_t workspace_bytes, void *stream);
 

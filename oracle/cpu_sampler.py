@@ -13,7 +13,13 @@ so that on the same fp32 inputs it produces the same scores bit for bit, and add
   an inverse CDF on a caller-supplied uniform ``u``;
 * per-row diagnostics that classify a row as a *boundary row* (the top-p crossing,
   a value tie or the CDF step lies within ``1e-6`` of the cut), which is the only
-  class of row whose token id may differ from a GPU implementation.
+  class of row whose token id may differ from a GPU implementation;
+* an exact evaluation of the top-p cut (float64 weights and cumulative sum over the
+  same sorted order).  The reference's fp32 ``softmax`` over a 151,936-entry row sums
+  to ``1 + delta`` with ``|delta|`` up to ~3e-5 (measured: the last element of its own
+  ``cumsum``), so its cut can differ from the exact one by a few tokens; the top-p
+  boundary band is therefore ``1e-6 + |delta|`` wide, and implementations are also
+  checked against the exact cut with the 1e-6 band.
 
 PyTorch facts this restatement relies on (probed on the installed torch CPU build):
 ``tensor / python_float`` is IEEE fp32 division by ``fp32(value)``;
@@ -45,14 +51,17 @@ class OracleRow:
     scores: torch.Tensor | None = None     # final scores (after penalties, T, top-k/p)
     kept: int = 0                          # number of finite final scores
     # boundary classification (sampled rows only)
-    topp_margin: float = math.inf          # |excl_cumsum - p| nearest the cut
+    topp_margin: float = math.inf          # |excl_cumsum - p| nearest the cut (reference arithmetic)
+    topp_norm_error: float = 0.0           # |sum of the reference's top-p probabilities - 1|
     topp_tie: bool = False                 # a value tie straddles the top-p cut
+    topp_exact_kept: int | None = None     # kept count of the exact (float64) top-p cut
+    topp_exact_margin: float = math.inf    # |exact excl - p| nearest the exact cut
     cdf_margin: float = math.inf           # |cdf step - u*Z| / Z nearest the token
     notes: list = field(default_factory=list)
 
     @property
     def boundary(self) -> bool:
-        return (self.topp_margin < BOUNDARY_EPS or self.topp_tie
+        return (self.topp_margin < BOUNDARY_EPS + self.topp_norm_error or self.topp_tie
                 or self.cdf_margin < BOUNDARY_EPS)
 
 
@@ -135,10 +144,11 @@ def restated_sample(logits: torch.Tensor, history=(), params=None, *, u: float |
         if p.top_p < 1:                                            # :56-59
             ordered, index = scores.sort(descending=True)
             probabilities = ordered.softmax(0)
-            excl = probabilities.cumsum(0) - probabilities
+            cumulative = probabilities.cumsum(0)
+            excl = cumulative - probabilities
             remove = excl > p.top_p
             if diagnostics:
-                _topp_diagnostics(row, ordered, excl, remove, p.top_p)
+                _topp_diagnostics(row, ordered, excl, remove, p.top_p, float(cumulative[-1]))
             scores[index[remove]] = -torch.inf
         probs = scores.softmax(0)                                  # :60
         row.probs = probs
@@ -161,9 +171,10 @@ def restated_sample(logits: torch.Tensor, history=(), params=None, *, u: float |
     return row
 
 
-def _topp_diagnostics(row: OracleRow, ordered, excl, remove, top_p) -> None:
-    """Distance of the top-p decision from its cut, and ties across the cut."""
-    p32 = float(np.float32(top_p))
+def _topp_diagnostics(row: OracleRow, ordered, excl, remove, top_p, total: float) -> None:
+    """Distance of the top-p decision from its cut, the reference's normalisation
+    error, ties across the cut, and the exact (float64) cut over the same order."""
+    p32 = float(np.float32(top_p))            # torch compares against fp32(top_p)
     e = excl.double().numpy()
     rm = remove.numpy()
     n = e.size
@@ -175,6 +186,18 @@ def _topp_diagnostics(row: OracleRow, ordered, excl, remove, top_p) -> None:
     row.topp_margin = min(margins) if margins else math.inf
     if 0 < first_removed < n:
         row.topp_tie = bool(ordered[first_removed - 1].item() == ordered[first_removed].item())
+    # the reference's probabilities are scaled by (1 + delta); its last cumsum entry is 1 + delta
+    o = ordered.double().numpy()
+    w = np.exp(o - o[0]) if np.isfinite(o[0]) else np.zeros_like(o)
+    z = w.sum()
+    if z > 0:
+        ex = (np.cumsum(w) - w) / z
+        row.topp_norm_error = abs(total - 1.0)
+        keep = ex <= p32
+        row.topp_exact_kept = int(keep.sum())
+        cut = row.topp_exact_kept
+        em = [abs(ex[j] - p32) for j in (cut - 1, cut) if 0 <= j < n and w[j] > 0]
+        row.topp_exact_margin = min(em) if em else math.inf
 
 
 def _cdf_diagnostics(row: OracleRow, probs, token: int, u: float) -> None:
