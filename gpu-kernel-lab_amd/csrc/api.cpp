@@ -82,7 +82,6 @@ bool make_plan(int32_t batch, int32_t vocab, int32_t dtype, int32_t max_top_k, i
     p->cand_cap = (int32_t)cap;
     const size_t B = (size_t)batch, S = (size_t)p->chunks;
     size_t off = 0;
-    p->off_count = off;   off = align_up(off + B * sizeof(uint32_t), 256);
     p->off_stats = off;   off = align_up(off + B * S * sizeof(ChunkStat), 256);
     p->off_cands = off;   off = align_up(off + B * S * (size_t)cap * sizeof(Cand), 256);
     p->off_rows = off;    off = align_up(off + B * sizeof(klsample_row_info), 256);
@@ -163,7 +162,6 @@ int klsample_run(const klsample_batch *b, void *stream) {
     a.probs = b->probs;
     a.row_info = b->row_info;
     unsigned char *ws = static_cast<unsigned char *>(b->workspace);
-    a.cand_count = reinterpret_cast<uint32_t *>(ws + plan.off_count);
     a.stats = reinterpret_cast<kls::ChunkStat *>(ws + plan.off_stats);
     a.cands = reinterpret_cast<kls::Cand *>(ws + plan.off_cands);
     a.rows = reinterpret_cast<klsample_row_info *>(ws + plan.off_rows);
@@ -172,7 +170,6 @@ int klsample_run(const klsample_batch *b, void *stream) {
     a.C = plan.chunk;
     a.S = plan.chunks;
     a.cand_cap = plan.cand_cap;
-    a.row_cap = plan.cand_cap * plan.chunks;
     a.vec_ok = (((uintptr_t)b->logits & 15u) == 0 && ((size_t)b->row_stride * esize) % 16 == 0) ? 1 : 0;
     a.xcd_map = (b->batch % 8 == 0) ? 1 : 0;
 

@@ -26,9 +26,9 @@ struct ChunkStat {
     float m;          // chunk max of the transformed scores (greedy / top-p / full rows)
     int32_t arg;      // lowest index attaining m (greedy rows)
     float y_thr;      // every element of the chunk with score >= y_thr is a candidate
-    int32_t ncand;    // candidates this chunk appended to the row's list
+    int32_t ncand;    // candidates written (capped at the slot capacity)
     double z;         // sum of exp(s - m) over the chunk
-    int32_t overflow; // unused (row-level overflow is cand_count > row_cap)
+    int32_t overflow; // candidates exceeded the slot capacity
     int32_t nfinite;  // elements with a finite score (greedy / top-p / full rows)
 };
 
@@ -43,7 +43,7 @@ struct Plan {
     int32_t chunk;    // elements per chunk (kThreads * E)
     int32_t chunks;   // chunks per row (S)
     int32_t cand_cap; // candidate slots per chunk
-    size_t off_count, off_stats, off_cands, off_rows, off_ybuf, total;
+    size_t off_stats, off_cands, off_rows, off_ybuf, total;
 };
 
 bool make_plan(int32_t batch, int32_t vocab, int32_t dtype, int32_t max_top_k, int32_t num_logprobs,
@@ -64,12 +64,11 @@ struct Args {
     float *top_lp;
     float *probs;
     klsample_row_info *row_info;
-    uint32_t *cand_count;  // per row: candidates appended by the streaming pass
     ChunkStat *stats;
-    Cand *cands;           // per row: S * cand_cap slots, filled in arrival order
+    Cand *cands;           // per (row, chunk): cand_cap slots
     klsample_row_info *rows;
     float *ybuf;
-    int32_t E, C, S, cand_cap, row_cap;
+    int32_t E, C, S, cand_cap;
     int32_t vec_ok;   // 16-byte vector loads are legal for every row
     int32_t xcd_map;  // place all chunks of a row on one XCD
 };

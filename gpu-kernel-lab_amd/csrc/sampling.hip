@@ -96,6 +96,8 @@ struct Misc {
         uint32_t u[kWaves];
         unsigned long long q[kWaves];
     } red;
+    float rf[2][kWaves];
+    int ri[2][kWaves];
     uint32_t hist[256];
     unsigned long long hmass[256];
     int topn_idx[kMaxLogprobs];
@@ -230,6 +232,17 @@ __device__ T block_excl_scan(T v, T *scratch, T &total) {
     return base + excl;
 }
 
+// Slot of the calling lane in an LDS list grown by `counter` (one LDS atomic per
+// wave); call it from the lanes that append.
+__device__ __forceinline__ int wave_append(int *counter) {
+    const unsigned long long bal = __ballot(true);
+    const int first = __ffsll((long long)bal) - 1;
+    int base = 0;
+    if (lane_id() == first) base = atomicAdd(counter, __popcll(bal));
+    base = __builtin_amdgcn_readlane(base, first);
+    return base + (int)__popcll(bal & ((1ull << lane_id()) - 1ull));
+}
+
 // ---------------------------------------------------------------------------------
 // Logits loaders: 16-byte vectors of fp32 (4) or bf16 (8) elements.
 template <typename TIn> struct Loader;
@@ -261,9 +274,19 @@ __device__ void build_counts(uint32_t *cnt, const Args &a, int row, int c0, int 
     for (int i = threadIdx.x; i < C / 4; i += kThreads) c4[i] = make_uint4(0u, 0u, 0u, 0u);
     __syncthreads();
     const int h0 = a.hist_off[row], h1 = a.hist_off[row + 1];
-    for (int h = h0 + (int)threadIdx.x; h < h1; h += kThreads) {
-        const unsigned rel = (unsigned)(a.hist_ids[h] - c0);
-        if (rel < (unsigned)cn) atomicAdd(&cnt[rel], 1u);
+    // eight independent loads in flight per thread before any LDS atomic
+    for (int hb = h0 + (int)threadIdx.x; hb < h1; hb += 8 * kThreads) {
+        int id[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int h = hb + j * kThreads;
+            id[j] = (h < h1) ? a.hist_ids[h] : -1;
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const unsigned rel = (unsigned)(id[j] - c0);
+            if (id[j] >= 0 && rel < (unsigned)cn) atomicAdd(&cnt[rel], 1u);
+        }
     }
     __syncthreads();
 }
@@ -371,10 +394,13 @@ __device__ float chunk_bound(const float (&x)[E], int K, uint32_t *keys, Misc &m
 // Radix selection over a row's entries.  A source enumerates (key, index, score)
 // for the entries it contains; each thread visits a disjoint subset.
 
-// The row's candidates: one contiguous list, read four entries per thread at a time.
+// The row's candidates in their per-chunk slots: chunk c holds cnt[c] entries (cnt in
+// LDS).  Waves take chunks round robin, four at a time, and lanes take a chunk's
+// entries, so the loads of four chunks are in flight together.
 struct CandSource {
     const Cand *cands;
-    int n;
+    const int *cnt;
+    int S, cap;
     float lo;
     template <class F>
     __device__ __forceinline__ void visit(uint2 e, F &f) const {
@@ -383,16 +409,42 @@ struct CandSource {
     }
     template <class F>
     __device__ void each(F f) const {
-        const uint2 *p = reinterpret_cast<const uint2 *>(cands);
-        int t = threadIdx.x;
-        for (; t + 3 * kThreads < n; t += 4 * kThreads) {
-            const uint2 e0 = p[t], e1 = p[t + kThreads], e2 = p[t + 2 * kThreads], e3 = p[t + 3 * kThreads];
-            visit(e0, f);
-            visit(e1, f);
-            visit(e2, f);
-            visit(e3, f);
+        const int lane = lane_id();
+        for (int c = wave_id(); c < S; c += 4 * kWaves) {
+            uint2 e[4];
+            bool v[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int cc = c + i * kWaves;
+                v[i] = cc < S && lane < cnt[cc];
+                if (v[i]) e[i] = reinterpret_cast<const uint2 *>(cands + (size_t)cc * cap)[lane];
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                if (v[i]) visit(e[i], f);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int cc = c + i * kWaves;
+                if (cc < S) {
+                    const uint2 *p = reinterpret_cast<const uint2 *>(cands + (size_t)cc * cap);
+                    for (int j = lane + 64; j < cnt[cc]; j += 64) visit(p[j], f);
+                }
+            }
         }
-        for (; t < n; t += kThreads) visit(p[t], f);
+    }
+};
+
+// n sort keys (desc_key) held in LDS.
+struct LdsSource {
+    const unsigned long long *sb;
+    int n;
+    template <class F>
+    __device__ void each(F f) const {
+        for (int i = threadIdx.x; i < n; i += kThreads) {
+            const unsigned long long k = sb[i];
+            const uint32_t key = ~(uint32_t)(k >> 32);
+            f(key, (int)(uint32_t)k, fkey_inv(key));
+        }
     }
 };
 
@@ -611,6 +663,35 @@ __device__ __forceinline__ unsigned long long desc_key(float y, int idx) {
 __device__ __forceinline__ float desc_key_y(unsigned long long k) { return fkey_inv(~(uint32_t)(k >> 32)); }
 __device__ __forceinline__ int desc_key_idx(unsigned long long k) { return (int)(uint32_t)k; }
 
+
+// Sort n <= kThreads distinct keys ascending in place: each thread ranks one key
+// against all n (LDS broadcast reads) and stores it at its rank.  Two barriers,
+// against ~log2(n)^2/2 for a bitonic network.
+__device__ void rank_sort(unsigned long long *sb, int n) {
+    const int t = threadIdx.x;
+    unsigned long long mine = 0ull;
+    int rank = 0;
+    if (t < n) {
+        mine = sb[t];
+        for (int j = 0; j < n; ++j) rank += (sb[j] < mine) ? 1 : 0;
+    }
+    __syncthreads();
+    if (t < n) sb[rank] = mine;
+    __syncthreads();
+}
+
+// Sort n distinct keys ascending in LDS (capacity >= pow2_ceil(n)).
+__device__ void sort_keys(unsigned long long *sb, int n) {
+    if (n <= 1) return;
+    if (n <= kThreads) {
+        rank_sort(sb, n);
+        return;
+    }
+    const int n2 = pow2_ceil(n);
+    for (int i = n + (int)threadIdx.x; i < n2; i += kThreads) sb[i] = ~0ull;
+    __syncthreads();
+    bitonic_sort(sb, n2);
+}
 
 // ---------------------------------------------------------------------------------
 // Outputs of a resolved row.
@@ -851,76 +932,177 @@ __device__ void dense_resolve(const Args &a, int row, const klsample_row_params 
 
 // Resolve one row from its chunk summaries and candidates (or hand it to
 // dense_resolve).  Runs in one workgroup of kThreads.
+// Copy the entries of `src` scoring >= lo into the LDS list `dst` (capacity cap);
+// returns how many there were (the list holds min(count, cap) of them).
+template <typename Src>
+__device__ int gather_keys(const Src &src, float lo, unsigned long long *dst, int cap, Misc &ms) {
+    if (threadIdx.x == 0) ms.ncand = 0;
+    __syncthreads();
+    src.each([&](uint32_t, int idx, float y) {
+        if (y >= lo) {
+            const int pos = wave_append(&ms.ncand);
+            if (pos < cap) dst[pos] = desc_key(y, idx);
+        }
+    });
+    __syncthreads();
+    return ms.ncand;
+}
+
+// Given D[0..n) sorted best first and the kept prefix length L, finish a sampled
+// row: normaliser, cut, top-N, inverse CDF in vocab order (D is reused as scratch).
+__device__ void finish_sampled(const Args &a, int row, int mode, const klsample_row_params &p,
+                               unsigned long long *D, int n, int L, double mref, Misc &ms) {
+    const int V = a.V;
+    RowOut r;
+    r.path = 0;
+    double zs = 0.0;
+    for (int i = threadIdx.x; i < L; i += kThreads) zs += exp((double)desc_key_y(D[i]) - mref);
+    const double zf = block_sumd(zs, ms);
+    const float cut_y = desc_key_y(D[L - 1]);
+    const bool partial = (L < n) && (desc_key_y(D[L]) == cut_y);
+    r.m = (float)mref;
+    r.cut = cut_y;
+    r.cut_idx = partial ? desc_key_idx(D[L - 1]) : V;
+    r.kept = L;
+    r.log_norm = log(zf);
+    const int count = min(a.N, L);
+    for (int t = threadIdx.x; t < count; t += kThreads) {
+        ms.topn_idx[t] = desc_key_idx(D[t]);
+        ms.topn_y[t] = desc_key_y(D[t]);
+    }
+    __syncthreads();
+    // the kept set in vocab order, then the first index whose cumulative weight
+    // exceeds u * zf
+    for (int i = threadIdx.x; i < L; i += kThreads) {
+        const unsigned long long k = D[i];
+        D[i] = ((unsigned long long)(uint32_t)desc_key_idx(k) << 32) | __float_as_uint(desc_key_y(k));
+    }
+    __syncthreads();
+    sort_keys(D, L);
+    int last;
+    double before;
+    int j = ordered_find(
+        L, [&](int i) { return exp((double)__uint_as_float((uint32_t)D[i]) - mref); },
+        (double)p.uniform * zf, ms, last, before);
+    if (j < 0) j = last >= 0 ? last : 0;
+    r.token = (int)(D[j] >> 32);
+    r.logprob = (double)__uint_as_float((uint32_t)D[j]) - mref - r.log_norm;
+    __syncthreads();
+    write_row(a, row, mode, r, count, ms);
+}
+
+// Length of the kept prefix of D[0..n) (sorted best first) under top-p: the first i
+// whose exclusive mass exceeds p * zref (the crossing entry is kept), or -1 if no
+// entry of D crosses.
+__device__ int topp_prefix(const unsigned long long *D, int n, double mref, double zref, float top_p, Misc &ms) {
+    const int seg = (n + kThreads - 1) / kThreads;
+    const int i0 = min((int)threadIdx.x * seg, n), i1 = min(i0 + seg, n);
+    double s = 0.0;
+    for (int i = i0; i < i1; ++i) s += exp((double)desc_key_y(D[i]) - mref);
+    double tot;
+    const double ex = block_excl_scan(s, ms.red.d, tot);
+    const double target = (double)top_p * zref;
+    int cut = 0x7fffffff;
+    double c = ex;
+    for (int i = i0; i < i1; ++i) {
+        if (cut == 0x7fffffff && c > target) cut = i;
+        c += exp((double)desc_key_y(D[i]) - mref);
+    }
+    cut = block_min(cut, ms);
+    return cut == 0x7fffffff ? -1 : cut;
+}
+
 // Resolve one row from its chunk summaries and candidates.  Runs in one workgroup
 // of kThreads.  Returns false when the candidates cannot settle the row (the caller
 // then runs dense_resolve).
 template <typename TIn, int E>
 __device__ bool combine_row(const Args &a, int row, const klsample_row_params &p, int mode,
-                            unsigned char *raw, Misc &ms) {
+                            unsigned char *raw, int *cnt, Misc &ms) {
     constexpr int C = kThreads * E;
     const int S = a.S, V = a.V, N = a.N;
-    if (a.options & KLSAMPLE_OPT_FORCE_DENSE) return false;
+    if ((a.options & KLSAMPLE_OPT_FORCE_DENSE) || S > kMaxChunksLds) return false;
     const ChunkStat *st = a.stats + (size_t)row * S;
-    const uint32_t listed = a.cand_count[row];
-    if (listed > (uint32_t)a.row_cap) return false;   // candidate list overflowed (massive ties)
 
+    // chunk summaries: (max, lo, finite count, overflow) then (sum-exp, argmax), each
+    // reduced over the workgroup with one LDS exchange
     float m = kNegInf, lo = kNegInf;
-    int arg = 0x7fffffff, nfinite = 0;
+    int nfinite = 0, ovf = 0;
     for (int c = threadIdx.x; c < S; c += kThreads) {
         const ChunkStat s = st[c];
         m = fmaxf(m, s.m);
         lo = fmaxf(lo, s.y_thr);
         nfinite += s.nfinite;
+        ovf |= s.overflow;
+        cnt[c] = min(s.ncand, a.cand_cap);
     }
-    m = block_max(m, ms);
-    lo = block_max(lo, ms);
-    nfinite = block_sum(nfinite, ms);
+    m = wave_reduce(m, OpMaxF(), kNegInf);
+    lo = wave_reduce(lo, OpMaxF(), kNegInf);
+    nfinite = wave_reduce(nfinite, OpSumI(), 0);
+    ovf = wave_reduce(ovf, OpOrI(), 0);
+    if (lane_id() == 0) {
+        ms.rf[0][wave_id()] = m; ms.rf[1][wave_id()] = lo;
+        ms.ri[0][wave_id()] = nfinite; ms.ri[1][wave_id()] = ovf;
+    }
+    __syncthreads();
+    m = ms.rf[0][0]; lo = ms.rf[1][0]; nfinite = ms.ri[0][0]; ovf = ms.ri[1][0];
+#pragma unroll
+    for (int w = 1; w < kWaves; ++w) {
+        m = fmaxf(m, ms.rf[0][w]); lo = fmaxf(lo, ms.rf[1][w]);
+        nfinite += ms.ri[0][w]; ovf |= ms.ri[1][w];
+    }
+    if (ovf) return false;   // a chunk's candidates overflowed (massive ties)
+    int arg = 0x7fffffff;
     double Z = 0.0;
     for (int c = threadIdx.x; c < S; c += kThreads) {
         const ChunkStat s = st[c];
         if (mode == kGreedy && s.m == m) arg = min(arg, s.arg);
         if (s.m > kNegInf) Z += s.z * exp((double)s.m - (double)m);
     }
-    arg = block_min(arg, ms);
-    Z = block_sumd(Z, ms);
+    arg = wave_reduce(arg, OpMinI(), 0x7fffffff);
+    Z = wave_reduce(Z, OpSumD(), 0.0);
+    __syncthreads();
+    if (lane_id() == 0) { ms.ri[0][wave_id()] = arg; ms.red.d[wave_id()] = Z; }
+    __syncthreads();
+    arg = ms.ri[0][0]; Z = ms.red.d[0];
+#pragma unroll
+    for (int w = 1; w < kWaves; ++w) { arg = min(arg, ms.ri[0][w]); Z += ms.red.d[w]; }
 
-    // candidate set F = { y >= lo }: complete above lo
-    CandSource src{a.cands + (size_t)row * a.row_cap, (int)listed, lo};
-    int nF = 0;
-    src.each([&](uint32_t, int, float) { ++nF; });
-    nF = block_sum(nF, ms);
-    const int R = (mode == kTopK) ? p.top_k : (mode == kTopP ? kSortCap / 2 : N);
+    // F = { candidates >= lo }: every element of the row scoring >= lo is in it
+    unsigned long long *A = reinterpret_cast<unsigned long long *>(raw);
+    unsigned long long *D = A + kSortCap;
+    const CandSource src{a.cands + (size_t)row * S * a.cand_cap, cnt, S, a.cand_cap, lo};
+    int nF = gather_keys(src, lo, A, kSortCap, ms);
     if (nF > kSortCap) {
-        if (R < 1 || R > kSortCap || R > nF) { return false; }
-        src.lo = fkey_inv(select_kth(src, (uint32_t)R, ms));
-        nF = 0;
-        src.each([&](uint32_t, int, float) { ++nF; });
-        nF = block_sum(nF, ms);
-        if (nF > kSortCap) { return false; }
+        const int R = (mode == kTopK) ? p.top_k : (mode == kTopP ? kThreads : N);
+        if (R < 1 || R > kSortCap) return false;
+        const float lo2 = fkey_inv(select_kth(src, (uint32_t)R, ms));
+        nF = gather_keys(src, lo2, A, kSortCap, ms);
+        if (nF > kSortCap) return false;
     }
-    unsigned long long *sb = reinterpret_cast<unsigned long long *>(raw);
-    if (threadIdx.x == 0) ms.ncand = 0;
-    __syncthreads();
-    src.each([&](uint32_t, int idx, float y) {
-        const int pos = atomicAdd(&ms.ncand, 1);
-        sb[pos] = desc_key(y, idx);
-    });
-    __syncthreads();
-    const int n2 = pow2_ceil(nF > 0 ? nF : 1);
-    for (int i = nF + (int)threadIdx.x; i < n2; i += kThreads) sb[i] = ~0ull;
-    __syncthreads();
-    bitonic_sort(sb, n2);
+    const LdsSource fsrc{A, nF};
+    const bool small = nF <= kThreads;   // sort the candidates outright
+    if (small) rank_sort(A, nF);
 
-    RowOut r;
-    r.path = 0;
-    int count = 0;
     if (mode == kGreedy || mode == kFull) {
-        count = min(N, nF);
-        for (int t = threadIdx.x; t < count; t += kThreads) {
-            ms.topn_idx[t] = desc_key_idx(sb[t]);
-            ms.topn_y[t] = desc_key_y(sb[t]);
+        int count = 0;
+        if (N > 0 && nF > 0) {
+            const int want = min(N, nF);
+            if (small) {
+                D = A;
+            } else {
+                const float tn = fkey_inv(select_kth(fsrc, (uint32_t)want, ms));
+                const int ng = gather_keys(fsrc, tn, D, kSortCap, ms);
+                sort_keys(D, ng);
+            }
+            count = want;
+            for (int t = threadIdx.x; t < count; t += kThreads) {
+                ms.topn_idx[t] = desc_key_idx(D[t]);
+                ms.topn_y[t] = desc_key_y(D[t]);
+            }
+            __syncthreads();
         }
-        __syncthreads();
+        RowOut r;
+        r.path = 0;
         r.m = m;
         r.cut = kNegInf;
         r.cut_idx = V;
@@ -941,21 +1123,22 @@ __device__ bool combine_row(const Args &a, int row, const klsample_row_params &p
             const ChunkStat sc = st[c];
             const int c0 = c * C, cn = min(C, V - c0);
             const bool pen = has_penalty(a, p, row);
-            uint32_t *cnt = reinterpret_cast<uint32_t *>(raw);
-            if (pen) build_counts<C>(cnt, a, row, c0, cn);
+            uint32_t *ctab = reinterpret_cast<uint32_t *>(raw);
+            __syncthreads();
+            if (pen) build_counts<C>(ctab, a, row, c0, cn);
             const double scale = exp((double)sc.m - (double)m);
             const double rem = (target - before) / scale;
             int lastj;
             double bj;
             int j = ordered_find(
                 cn, [&](int i) {
-                    const float y = element_final<TIn>(a, p, row, c0 + i, pen ? cnt : nullptr, c0, true);
+                    const float y = element_final<TIn>(a, p, row, c0 + i, pen ? ctab : nullptr, c0, true);
                     return (double)exp_fast(y - sc.m);
                 },
                 rem, ms, lastj, bj);
             if (j < 0) j = lastj >= 0 ? lastj : 0;
             r.token = c0 + j;
-            const float yt = element_final<TIn>(a, p, row, r.token, pen ? cnt : nullptr, c0, true);
+            const float yt = element_final<TIn>(a, p, row, r.token, pen ? ctab : nullptr, c0, true);
             r.logprob = (double)yt - (double)m - r.log_norm;
             __syncthreads();
         }
@@ -963,86 +1146,77 @@ __device__ bool combine_row(const Args &a, int row, const klsample_row_params &p
         return true;
     }
 
-    // top-k (optionally followed by top-p) or top-p alone, over the sorted candidates
-    int L0;
-    double mref;
-    if (mode == kTopK) {
-        const int kk = p.top_k;
-        const float tau = (nF >= kk) ? desc_key_y(sb[kk - 1]) : kNegInf;
-        int c = 0;
-        for (int i = threadIdx.x; i < nF; i += kThreads) c += (desc_key_y(sb[i]) >= tau) ? 1 : 0;
-        L0 = block_sum(c, ms);
-        mref = nF > 0 ? (double)desc_key_y(sb[0]) : 0.0;
-    } else {
-        L0 = nF;
-        mref = (double)m;
-    }
-    if (L0 == 0) {
+    if (nF == 0) {
         // every score is -inf: nothing can be drawn
-        r.m = m; r.cut = kNegInf; r.cut_idx = V; r.kept = 0; r.log_norm = 0.0;
+        RowOut r;
+        r.path = 0; r.m = m; r.cut = kNegInf; r.cut_idx = V; r.kept = 0; r.log_norm = 0.0;
         r.token = 0; r.logprob = __builtin_nan("");
         write_row(a, row, mode, r, 0, ms);
         return true;
     }
-    const int seg = (L0 + kThreads - 1) / kThreads;
-    const int i0 = min((int)threadIdx.x * seg, L0), i1 = min(i0 + seg, L0);
-    double s = 0.0;
-    for (int i = i0; i < i1; ++i) s += exp((double)desc_key_y(sb[i]) - mref);
-    double tot;
-    const double ex = block_excl_scan(s, ms.red.d, tot);
-    const double zref = (mode == kTopK) ? tot : Z;
-    int L = L0;
-    if (p.flags & KLSAMPLE_ROW_TOP_P) {
-        const double target = (double)p.top_p * zref;
-        int cut = 0x7fffffff;
-        double c = ex;
-        for (int i = i0; i < i1; ++i) {
-            if (cut == 0x7fffffff && c > target) cut = i;
-            c += exp((double)desc_key_y(sb[i]) - mref);
+
+    if (mode == kTopK) {
+        // top-k: every candidate >= the kk-th largest (ties included), sorted
+        const int kk = p.top_k;
+        int lk;
+        if (small) {
+            // A is sorted: the kept prefix runs to the last tie of the kk-th entry
+            D = A;
+            lk = nF;
+            if (nF > kk) {
+                const float tau = desc_key_y(A[kk - 1]);
+                int c = 0;
+                for (int i = kk + (int)threadIdx.x; i < nF; i += kThreads) c += (desc_key_y(A[i]) == tau) ? 1 : 0;
+                lk = kk + block_sum(c, ms);
+            }
+        } else {
+            const float tau = (nF > kk) ? fkey_inv(select_kth(fsrc, (uint32_t)kk, ms)) : kNegInf;
+            lk = gather_keys(fsrc, tau, D, kSortCap, ms);
+            sort_keys(D, lk);
         }
-        cut = block_min(cut, ms);
-        if (cut != 0x7fffffff) {
-            L = cut;
-        } else if (mode == kTopP && lo > kNegInf) {
-            // the kept mass reaches past the complete candidate region
-            return false;
+        const double mref = (double)desc_key_y(D[0]);
+        int L = lk;
+        if (p.flags & KLSAMPLE_ROW_TOP_P) {
+            double zs = 0.0;
+            for (int i = threadIdx.x; i < lk; i += kThreads) zs += exp((double)desc_key_y(D[i]) - mref);
+            const double zk = block_sumd(zs, ms);
+            const int cut = topp_prefix(D, lk, mref, zk, p.top_p, ms);
+            if (cut > 0) L = cut;
+        }
+        finish_sampled(a, row, mode, p, D, lk, L, mref, ms);
+        return true;
+    }
+
+    // top-p alone: walk the best kThreads first, then every candidate
+    const double mref = (double)m;
+    int n = 0, L = -1;
+    if (small) {
+        D = A;
+        n = nF;
+        L = topp_prefix(D, n, mref, Z, p.top_p, ms);
+        if (L < 0) {
+            if (lo > kNegInf) return false;
+            L = n;
+        }
+        finish_sampled(a, row, mode, p, D, n, L, mref, ms);
+        return true;
+    }
+    const float t256 = fkey_inv(select_kth(fsrc, (uint32_t)kThreads, ms));
+    n = gather_keys(fsrc, t256, D, kSortCap, ms);
+    sort_keys(D, n);
+    L = topp_prefix(D, n, mref, Z, p.top_p, ms);
+    if (L < 0) {
+        for (int i = threadIdx.x; i < nF; i += kThreads) D[i] = A[i];
+        __syncthreads();
+        n = nF;
+        sort_keys(D, n);
+        L = topp_prefix(D, n, mref, Z, p.top_p, ms);
+        if (L < 0) {
+            if (lo > kNegInf) return false;   // the kept mass reaches past the candidates
+            L = n;                            // the candidates are the whole row
         }
     }
-    double zs = 0.0;
-    for (int i = i0; i < min(i1, L); ++i) zs += exp((double)desc_key_y(sb[i]) - mref);
-    const double zf = block_sumd(zs, ms);
-    const float cut_y = desc_key_y(sb[L - 1]);
-    const bool partial = (L < nF) && (desc_key_y(sb[L]) == cut_y);
-    r.m = (float)mref;
-    r.cut = cut_y;
-    r.cut_idx = partial ? desc_key_idx(sb[L - 1]) : V;
-    r.kept = L;
-    r.log_norm = log(zf);
-    count = min(N, L);
-    for (int t = threadIdx.x; t < count; t += kThreads) {
-        ms.topn_idx[t] = desc_key_idx(sb[t]);
-        ms.topn_y[t] = desc_key_y(sb[t]);
-    }
-    __syncthreads();
-    // inverse CDF over the kept set in vocab order
-    for (int i = threadIdx.x; i < L; i += kThreads) {
-        const unsigned long long k = sb[i];
-        sb[i] = ((unsigned long long)(uint32_t)desc_key_idx(k) << 32) | __float_as_uint(desc_key_y(k));
-    }
-    const int l2 = pow2_ceil(L);
-    for (int i = L + (int)threadIdx.x; i < l2; i += kThreads) sb[i] = ~0ull;
-    __syncthreads();
-    bitonic_sort(sb, l2);
-    int last;
-    double before;
-    int j = ordered_find(
-        L, [&](int i) { return exp((double)__uint_as_float((uint32_t)sb[i]) - mref); },
-        (double)p.uniform * zf, ms, last, before);
-    if (j < 0) j = last >= 0 ? last : 0;
-    r.token = (int)(sb[j] >> 32);
-    r.logprob = (double)__uint_as_float((uint32_t)sb[j]) - mref - r.log_norm;
-    __syncthreads();
-    write_row(a, row, mode, r, count, ms);
+    finish_sampled(a, row, mode, p, D, n, L, mref, ms);
     return true;
 }
 
@@ -1070,7 +1244,7 @@ struct ScanLds {
 template <int C>
 struct RowLds {
     static constexpr int a = C * 4;
-    static constexpr int b = kSortCap * 8;
+    static constexpr int b = 2 * kSortCap * 8;
     static constexpr int value = a > b ? a : b;
 };
 
@@ -1191,12 +1365,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
         int wbase = 0;
         if (lane_id() == 0 && wtot > 0) wbase = atomicAdd(&ms.ncand, wtot);
         wbase = readlane(wbase, 0);
-        __syncthreads();
-        // one append per workgroup to the row's contiguous candidate list
-        if (tid == 0) ms.ia = ms.ncand > 0 ? (int)atomicAdd(&a.cand_count[row], (uint32_t)ms.ncand) : 0;
-        __syncthreads();
-        int pos = ms.ia + wbase + incl - my;
-        Cand *out = a.cands + (size_t)row * a.row_cap;
+        int pos = wbase + incl - my;
+        Cand *out = a.cands + ((size_t)row * a.S + chunk) * a.cand_cap;
 #pragma unroll
         for (int v = 0; v < NV; ++v) {
             const int li = (v * kThreads + tid) * VW;
@@ -1204,7 +1374,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
             for (int e = 0; e < VW; ++e) {
                 const float xv = x[v * VW + e];
                 if (xv >= thr && xv > kNegInf) {
-                    if (pos < a.row_cap) {
+                    if (pos < a.cand_cap) {
                         Cand cd;
                         cd.y = (mode == kTopK) ? __fdiv_rn(xv, p.temperature) : xv;
                         cd.idx = c0 + li + e;
@@ -1214,7 +1384,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
                 }
             }
         }
-        st.ncand = ms.ncand;
+        __syncthreads();
+        st.ncand = min(ms.ncand, a.cand_cap);
+        st.overflow = ms.ncand > a.cand_cap ? 1 : 0;
     }
     if (tid == 0) a.stats[(size_t)row * a.S + chunk] = st;
 }
@@ -1224,13 +1396,12 @@ template <typename TIn, int E>
 __global__ __launch_bounds__(kThreads) void row_kernel(Args a) {
     constexpr int C = kThreads * E;
     __shared__ __attribute__((aligned(16))) unsigned char raw[RowLds<C>::value];
+    __shared__ int cnt[kMaxChunksLds];
     __shared__ Misc ms;
     const int row = blockIdx.x;
     const klsample_row_params p = a.params[row];
     const int mode = row_mode(p, a.V);
-    if (!combine_row<TIn, E>(a, row, p, mode, raw, ms)) dense_resolve<TIn, E>(a, row, p, mode, raw, ms);
-    // leave the row's candidate list empty for the next call (read once, at the start)
-    if (threadIdx.x == 0) a.cand_count[row] = 0u;
+    if (!combine_row<TIn, E>(a, row, p, mode, raw, cnt, ms)) dense_resolve<TIn, E>(a, row, p, mode, raw, ms);
 }
 
 // Final probabilities: exp(s - max - log_norm) on the kept set, 0 elsewhere.

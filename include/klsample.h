@@ -110,9 +110,9 @@ int klsample_abi_version(void);
 int klsample_workspace_size(int32_t batch, int32_t vocab, int32_t dtype, int32_t max_top_k,
                             int32_t num_logprobs, size_t *bytes);
 
-/* Zero-fill a workspace before its first use (enqueued on `stream`, a hipStream_t).
- * A call leaves the workspace ready for the next one, so this is needed once per
- * allocation. */
+/* Zero-fill a workspace (enqueued on `stream`, a hipStream_t).  klsample_run does not
+ * require it (a call writes every workspace byte it later reads); it makes the
+ * workspace contents reproducible for inspection. */
 int klsample_workspace_init(void *workspace, size_t workspace_bytes, void *stream);
 
 /* Sample one token per row; enqueued on `stream` (a hipStream_t, NULL = default).
