@@ -13,6 +13,8 @@
 namespace {
 
 thread_local std::string g_last_error;
+thread_local kls::PhaseEvents g_phases;   // diagnostic events of this thread's calls
+thread_local bool g_phases_on = false;
 
 int fail(int status, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
 int fail(int status, const char *fmt, ...) {
@@ -98,6 +100,14 @@ int klsample_abi_version(void) { return KLSAMPLE_ABI_VERSION; }
 
 const char *klsample_last_error(void) { return g_last_error.c_str(); }
 
+int klsample_set_phase_events(void *const *events, int32_t count) {
+    if (count < 0 || count > 4) return fail(KLSAMPLE_ERR_INVALID_ARGUMENT, "count must be in [0, 4] (got %d)", count);
+    if (count > 0 && events == nullptr) return fail(KLSAMPLE_ERR_INVALID_ARGUMENT, "events must not be NULL");
+    for (int i = 0; i < 4; ++i) g_phases.ev[i] = i < count ? static_cast<hipEvent_t>(events[i]) : nullptr;
+    g_phases_on = count > 0;
+    return ok();
+}
+
 int klsample_workspace_size(int32_t batch, int32_t vocab, int32_t dtype, int32_t max_top_k, int32_t num_logprobs,
                             size_t *bytes) {
     if (bytes == nullptr) return fail(KLSAMPLE_ERR_INVALID_ARGUMENT, "bytes must not be NULL");
@@ -173,7 +183,8 @@ int klsample_run(const klsample_batch *b, void *stream) {
     a.vec_ok = (((uintptr_t)b->logits & 15u) == 0 && ((size_t)b->row_stride * esize) % 16 == 0) ? 1 : 0;
     a.xcd_map = (b->batch % 8 == 0) ? 1 : 0;
 
-    const hipError_t e = kls::launch_sample(a, b->dtype, static_cast<hipStream_t>(stream));
+    const hipError_t e = kls::launch_sample(a, b->dtype, static_cast<hipStream_t>(stream),
+                                           g_phases_on ? &g_phases : nullptr);
     if (e != hipSuccess) return fail(KLSAMPLE_ERR_HIP, "kernel launch failed: %s", hipGetErrorString(e));
     return ok();
 }

@@ -73,7 +73,14 @@ struct Args {
     int32_t xcd_map;  // place all chunks of a row on one XCD
 };
 
-hipError_t launch_sample(const Args &args, int32_t dtype, hipStream_t stream);
+// Caller-owned hipEvent_t handles recorded around the kernels of a call (diagnostics):
+// ev[0] before the streaming pass, ev[1] after it, ev[2] after the row combine,
+// ev[3] after the optional probability write-out.  NULL entries are skipped.
+struct PhaseEvents {
+    hipEvent_t ev[4];
+};
+
+hipError_t launch_sample(const Args &args, int32_t dtype, hipStream_t stream, const PhaseEvents *phases);
 hipError_t launch_zero_fill(void *ptr, size_t bytes, hipStream_t stream);
 
 }  // namespace kls

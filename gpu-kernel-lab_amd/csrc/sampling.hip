@@ -1435,30 +1435,40 @@ __global__ void zero_fill_kernel(uint4 *p, size_t n16, unsigned char *tail, size
         for (size_t i = threadIdx.x; i < ntail; i += blockDim.x) tail[i] = 0;
 }
 
+hipError_t mark(const PhaseEvents *ph, int i, hipStream_t s) {
+    if (ph == nullptr || ph->ev[i] == nullptr) return hipSuccess;
+    return hipEventRecord(ph->ev[i], s);
+}
+
 template <typename TIn, int E>
-hipError_t launch_typed(const Args &a, hipStream_t s) {
+hipError_t launch_typed(const Args &a, hipStream_t s, const PhaseEvents *ph) {
     const dim3 grid((unsigned)((int64_t)a.B * a.S));
+    hipError_t e = mark(ph, 0, s);
+    if (e != hipSuccess) return e;
     scan_kernel<TIn, E><<<grid, kThreads, 0, s>>>(a);
+    if ((e = mark(ph, 1, s)) != hipSuccess) return e;
     row_kernel<TIn, E><<<dim3((unsigned)a.B), kThreads, 0, s>>>(a);
+    if ((e = mark(ph, 2, s)) != hipSuccess) return e;
     if (a.probs) probs_kernel<TIn, E><<<grid, kThreads, 0, s>>>(a);
+    if ((e = mark(ph, 3, s)) != hipSuccess) return e;
     return hipGetLastError();
 }
 
 }  // namespace
 
-hipError_t launch_sample(const Args &a, int32_t dtype, hipStream_t s) {
+hipError_t launch_sample(const Args &a, int32_t dtype, hipStream_t s, const PhaseEvents *ph) {
     if (dtype == KLSAMPLE_FLOAT32) {
         switch (a.E) {
-            case 4: return launch_typed<float, 4>(a, s);
-            case 8: return launch_typed<float, 8>(a, s);
-            case 16: return launch_typed<float, 16>(a, s);
-            case 32: return launch_typed<float, 32>(a, s);
+            case 4: return launch_typed<float, 4>(a, s, ph);
+            case 8: return launch_typed<float, 8>(a, s, ph);
+            case 16: return launch_typed<float, 16>(a, s, ph);
+            case 32: return launch_typed<float, 32>(a, s, ph);
         }
     } else {
         switch (a.E) {
-            case 8: return launch_typed<uint16_t, 8>(a, s);
-            case 16: return launch_typed<uint16_t, 16>(a, s);
-            case 32: return launch_typed<uint16_t, 32>(a, s);
+            case 8: return launch_typed<uint16_t, 8>(a, s, ph);
+            case 16: return launch_typed<uint16_t, 16>(a, s, ph);
+            case 32: return launch_typed<uint16_t, 32>(a, s, ph);
         }
     }
     return hipErrorInvalidValue;

@@ -123,6 +123,15 @@ int klsample_workspace_init(void *workspace, size_t workspace_bytes, void *strea
  * exceeds uniform * total. */
 int klsample_run(const klsample_batch *batch, void *stream);
 
+/* Diagnostic timing; no reference counterpart.  With count in [1, 4], every later
+ * klsample_run issued from this thread records events[i] (hipEvent_t handles owned by
+ * the caller, NULL entries skipped) on its stream: events[0] before the streaming pass
+ * over the logits, events[1] after it, events[2] after the per-row combine and
+ * events[3] after the optional probability write-out.  The handles are copied; count
+ * 0 turns recording off.  Each recording costs a stream marker, so timed calls are
+ * slightly slower than unrecorded ones. */
+int klsample_set_phase_events(void *const *events, int32_t count);
+
 /* Description of the last failure on this thread ("" if none). */
 const char *klsample_last_error(void);
 

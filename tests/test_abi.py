@@ -74,6 +74,18 @@ def test_workspace_size_validation(lib):
     assert lib.klsample_workspace_size(1, 10, 0, 0, 0, None) == _lib.ERR_INVALID_ARGUMENT
 
 
+def test_phase_event_hook_validation(lib):
+    """The hook only stores handles; nothing reaches HIP until a run records them."""
+    assert lib.klsample_set_phase_events(None, 0) == _lib.OK
+    assert lib.klsample_set_phase_events(None, 1) == _lib.ERR_INVALID_ARGUMENT
+    assert 'events' in _lib.last_error(lib)
+    handles = (ctypes.c_void_p * 5)()
+    assert lib.klsample_set_phase_events(handles, 5) == _lib.ERR_INVALID_ARGUMENT
+    assert lib.klsample_set_phase_events(handles, -1) == _lib.ERR_INVALID_ARGUMENT
+    assert lib.klsample_set_phase_events(handles, 4) == _lib.OK   # all NULL: nothing recorded
+    assert lib.klsample_set_phase_events(None, 0) == _lib.OK
+
+
 def test_workspace_grows_with_work(lib):
     base = _size(lib, 8, 151936)[1]
     assert _size(lib, 256, 151936)[1] > base
