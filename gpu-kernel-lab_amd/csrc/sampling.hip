@@ -87,8 +87,9 @@ __device__ __forceinline__ bool has_penalty(const Args &a, const klsample_row_pa
 }
 
 // ---------------------------------------------------------------------------------
-// LDS scratch shared by all phases of a workgroup.
-struct Misc {
+// LDS scratch shared by all phases of a workgroup.  Red is the cross-wave exchange
+// slot of the block reductions.
+struct Red {
     union {
         float f[kWaves];
         double d[kWaves];
@@ -96,6 +97,17 @@ struct Misc {
         uint32_t u[kWaves];
         unsigned long long q[kWaves];
     } red;
+};
+
+// The streaming pass needs little beyond the reductions (its LDS footprint sets how
+// many workgroups share a CU).
+struct ScanMisc : Red {
+    uint32_t bound_key;
+    int ncand;
+    int nhits;
+};
+
+struct Misc : Red {
     float rf[2][kWaves];
     int ri[2][kWaves];
     uint32_t hist[256];
@@ -112,6 +124,7 @@ struct Misc {
     uint32_t sel_above_count;
     int sel_found;
     int ia, ib;
+    uint32_t kmin, kmax;
     double da, db;
 };
 
@@ -181,7 +194,7 @@ template <typename T>
 __device__ __forceinline__ T wave_shift_excl(T incl) { return dpp<0x138>(T(0), incl); }  // wave_shr:1
 
 template <typename T, typename Op>
-__device__ T block_reduce(T v, Op op, T *scratch, T id) {
+__device__ __forceinline__ T block_reduce(T v, Op op, T *scratch, T id) {
     v = wave_reduce(v, op, id);
     __syncthreads();
     if (lane_id() == 0) scratch[wave_id()] = v;
@@ -201,20 +214,22 @@ struct OpSumQ {
     __device__ unsigned long long operator()(unsigned long long a, unsigned long long b) const { return a + b; }
 };
 struct OpOrI { __device__ int operator()(int a, int b) const { return a | b; } };
+struct OpMinU { __device__ uint32_t operator()(uint32_t a, uint32_t b) const { return a < b ? a : b; } };
+struct OpMaxU { __device__ uint32_t operator()(uint32_t a, uint32_t b) const { return a > b ? a : b; } };
 
-__device__ __forceinline__ float block_max(float v, Misc &ms) { return block_reduce(v, OpMaxF(), ms.red.f, kNegInf); }
-__device__ __forceinline__ int block_min(int v, Misc &ms) { return block_reduce(v, OpMinI(), ms.red.i, 0x7fffffff); }
-__device__ __forceinline__ int block_maxi(int v, Misc &ms) { return block_reduce(v, OpMaxI(), ms.red.i, (int)0x80000000); }
-__device__ __forceinline__ int block_sum(int v, Misc &ms) { return block_reduce(v, OpSumI(), ms.red.i, 0); }
-__device__ __forceinline__ int block_or(int v, Misc &ms) { return block_reduce(v, OpOrI(), ms.red.i, 0); }
-__device__ __forceinline__ double block_sumd(double v, Misc &ms) { return block_reduce(v, OpSumD(), ms.red.d, 0.0); }
-__device__ __forceinline__ unsigned long long block_sumq(unsigned long long v, Misc &ms) {
+__device__ __forceinline__ float block_max(float v, Red &ms) { return block_reduce(v, OpMaxF(), ms.red.f, kNegInf); }
+__device__ __forceinline__ int block_min(int v, Red &ms) { return block_reduce(v, OpMinI(), ms.red.i, 0x7fffffff); }
+__device__ __forceinline__ int block_maxi(int v, Red &ms) { return block_reduce(v, OpMaxI(), ms.red.i, (int)0x80000000); }
+__device__ __forceinline__ int block_sum(int v, Red &ms) { return block_reduce(v, OpSumI(), ms.red.i, 0); }
+__device__ __forceinline__ int block_or(int v, Red &ms) { return block_reduce(v, OpOrI(), ms.red.i, 0); }
+__device__ __forceinline__ double block_sumd(double v, Red &ms) { return block_reduce(v, OpSumD(), ms.red.d, 0.0); }
+__device__ __forceinline__ unsigned long long block_sumq(unsigned long long v, Red &ms) {
     return block_reduce(v, OpSumQ(), ms.red.q, 0ull);
 }
 
 // Exclusive scan over the workgroup in thread order; `total` receives the sum.
 template <typename T>
-__device__ T block_excl_scan(T v, T *scratch, T &total) {
+__device__ __forceinline__ T block_excl_scan(T v, T *scratch, T &total) {
     const T incl = wave_incl_scan(v);
     const T excl = wave_shift_excl(incl);
     const T wt = readlane(incl, 63);
@@ -269,7 +284,7 @@ template <> struct Loader<uint16_t> {
 
 // Count table of the row's history restricted to [c0, c0 + cn): cnt[i - c0].
 template <int C>
-__device__ void build_counts(uint32_t *cnt, const Args &a, int row, int c0, int cn) {
+__device__ __forceinline__ void build_counts(uint32_t *cnt, const Args &a, int row, int c0, int cn) {
     uint4 *c4 = reinterpret_cast<uint4 *>(cnt);
     for (int i = threadIdx.x; i < C / 4; i += kThreads) c4[i] = make_uint4(0u, 0u, 0u, 0u);
     __syncthreads();
@@ -311,7 +326,7 @@ __device__ __forceinline__ float element_final(const Args &a, const klsample_row
 // kThreads*G disjoint groups (E/G consecutive register elements per group).  K groups
 // have a maximum at or above it, so at least K elements are.
 template <int E, int G>
-__device__ float group_bound(const float (&x)[E], int K, uint32_t *keys, Misc &ms) {
+__device__ __forceinline__ float group_bound(const float (&x)[E], int K, uint32_t *keys, ScanMisc &ms) {
     constexpr int GS = E / G;
     constexpr int NG = kThreads * G;
     constexpr int PER = NG / 64;   // keys per lane of the counting wave
@@ -362,7 +377,7 @@ __device__ float group_bound(const float (&x)[E], int K, uint32_t *keys, Misc &m
 }
 
 template <int E>
-__device__ float group_bound_dispatch(const float (&x)[E], int G, int K, uint32_t *keys, Misc &ms) {
+__device__ __forceinline__ float group_bound_dispatch(const float (&x)[E], int G, int K, uint32_t *keys, ScanMisc &ms) {
     switch (G) {
         case 1: return group_bound<E, 1>(x, K, keys, ms);
         case 2: if constexpr (E >= 2) return group_bound<E, 2>(x, K, keys, ms); break;
@@ -377,7 +392,7 @@ __device__ float group_bound_dispatch(const float (&x)[E], int G, int K, uint32_
 // start as coarse as 4K groups allow and are refined while fewer than K of them hold a
 // finite element (a partial last chunk, masked logits).
 template <int E>
-__device__ float chunk_bound(const float (&x)[E], int K, uint32_t *keys, Misc &ms) {
+__device__ __forceinline__ float chunk_bound(const float (&x)[E], int K, uint32_t *keys, ScanMisc &ms) {
     constexpr int kMaxG = (E < kMaxGroupKeys / kThreads) ? E : kMaxGroupKeys / kThreads;
     int G = 1;
     while (G < kMaxG && G * kThreads < 4 * K) G <<= 1;
@@ -397,14 +412,17 @@ __device__ float chunk_bound(const float (&x)[E], int K, uint32_t *keys, Misc &m
 // The row's candidates in their per-chunk slots: chunk c holds cnt[c] entries (cnt in
 // LDS).  Waves take chunks round robin, four at a time, and lanes take a chunk's
 // entries, so the loads of four chunks are in flight together.
+// Top-k rows store their candidates before the division by T (`temp` > 0 divides).
 struct CandSource {
     const Cand *cands;
     const int *cnt;
     int S, cap;
     float lo;
+    float temp;
     template <class F>
     __device__ __forceinline__ void visit(uint2 e, F &f) const {
-        const float y = __uint_as_float(e.x);
+        float y = __uint_as_float(e.x);
+        if (temp > 0.f) y = __fdiv_rn(y, temp);
         if (y >= lo) f(fkey(y), (int)e.y, y);
     }
     template <class F>
@@ -467,7 +485,7 @@ struct DenseSource {
 
 // Wave 0 scans 256 histogram bins from the highest digit down and records the
 // first bin at which the running count reaches `need`.
-__device__ void pick_digit_count(Misc &ms, uint32_t need) {
+__device__ __forceinline__ void pick_digit_count(Misc &ms, uint32_t need) {
     if (threadIdx.x < 64) {
         const int l = lane_id();
         uint32_t c[4], s = 0;
@@ -495,7 +513,7 @@ __device__ void pick_digit_count(Misc &ms, uint32_t need) {
 
 // Key of the R-th largest entry of `src` (R >= 1, R <= number of entries).
 template <typename Src>
-__device__ uint32_t select_kth(const Src &src, uint32_t R, Misc &ms) {
+__device__ __forceinline__ uint32_t select_kth(const Src &src, uint32_t R, Misc &ms) {
     uint32_t prefix = 0u, need = R;
     for (int shift = 24; shift >= 0; shift -= 8) {
         const uint32_t hmask = (shift == 24) ? 0u : (0xffffffffu << (shift + 8));
@@ -525,7 +543,7 @@ struct MassPick {
 };
 
 template <typename Src>
-__device__ bool select_mass(const Src &src, double target, double m, MassPick &out, Misc &ms) {
+__device__ __forceinline__ bool select_mass(const Src &src, double target, double m, MassPick &out, Misc &ms) {
     uint32_t prefix = 0u;
     unsigned long long above = 0ull;
     uint32_t above_count = 0u;
@@ -594,7 +612,7 @@ __device__ bool select_mass(const Src &src, double target, double m, MassPick &o
 // inclusive cumulative weight exceeds `target`, or -1; `last` receives the last item
 // with positive weight (-1 if none).
 template <typename W>
-__device__ int ordered_find(int n, W weight, double target, Misc &ms, int &last, double &before) {
+__device__ __forceinline__ int ordered_find(int n, W weight, double target, Misc &ms, int &last, double &before) {
     double base = 0.0;
     int lastp = -1;
     for (int t0 = 0; t0 < n; t0 += kThreads * 4) {
@@ -634,7 +652,7 @@ __device__ int ordered_find(int n, W weight, double target, Misc &ms, int &last,
 }
 
 // Bitonic sort (ascending) of n = power of two 64-bit keys in LDS.
-__device__ void bitonic_sort(unsigned long long *s, int n) {
+__device__ __forceinline__ void bitonic_sort(unsigned long long *s, int n) {
     for (int k = 2; k <= n; k <<= 1) {
         for (int j = k >> 1; j > 0; j >>= 1) {
             for (int i = threadIdx.x; i < n; i += kThreads) {
@@ -656,6 +674,21 @@ __device__ __forceinline__ int pow2_ceil(int n) {
     return p;
 }
 
+// A chunk summary as two 16-byte loads (one request per half, never split or predicated).
+__device__ __forceinline__ ChunkStat load_stat(const ChunkStat *p) {
+    const uint4 *q = reinterpret_cast<const uint4 *>(p);
+    const uint4 u = q[0], v = q[1];
+    ChunkStat s;
+    s.m = __uint_as_float(u.x);
+    s.arg = (int32_t)u.y;
+    s.y_thr = __uint_as_float(u.z);
+    s.ncand = (int32_t)u.w;
+    s.z = __hiloint2double((int)v.y, (int)v.x);
+    s.overflow = (int32_t)v.z;
+    s.nfinite = (int32_t)v.w;
+    return s;
+}
+
 // Sort key: ascending order = score descending, then index ascending.
 __device__ __forceinline__ unsigned long long desc_key(float y, int idx) {
     return ((unsigned long long)(~fkey(y)) << 32) | (uint32_t)idx;
@@ -667,7 +700,7 @@ __device__ __forceinline__ int desc_key_idx(unsigned long long k) { return (int)
 // Sort n <= kThreads distinct keys ascending in place: each thread ranks one key
 // against all n (LDS broadcast reads) and stores it at its rank.  Two barriers,
 // against ~log2(n)^2/2 for a bitonic network.
-__device__ void rank_sort(unsigned long long *sb, int n) {
+__device__ __forceinline__ void rank_sort(unsigned long long *sb, int n) {
     const int t = threadIdx.x;
     unsigned long long mine = 0ull;
     int rank = 0;
@@ -681,7 +714,7 @@ __device__ void rank_sort(unsigned long long *sb, int n) {
 }
 
 // Sort n distinct keys ascending in LDS (capacity >= pow2_ceil(n)).
-__device__ void sort_keys(unsigned long long *sb, int n) {
+__device__ __forceinline__ void sort_keys(unsigned long long *sb, int n) {
     if (n <= 1) return;
     if (n <= kThreads) {
         rank_sort(sb, n);
@@ -711,7 +744,7 @@ struct RowOut {
 // from ms.topn_* (`count` finite entries, best first).  Slots from `count` up to
 // min(N, V) are -inf entries whose ids are the smallest not already listed;
 // slots beyond min(N, V) (only when V < N) hold id -1.
-__device__ void write_row(const Args &a, int row, int mode, const RowOut &r, int count, Misc &ms) {
+__device__ __forceinline__ void write_row(const Args &a, int row, int mode, const RowOut &r, int count, Misc &ms) {
     const int N = a.N, V = a.V;
     if (N > 0) {
         const int nv = min(N, V);
@@ -766,7 +799,7 @@ __device__ void write_row(const Args &a, int row, int mode, const RowOut &r, int
 
 // Top-N of the entries of a dense source, best first, into ms.topn_*; ties at the
 // N-th score are taken in index order.  Returns the number written.
-__device__ int dense_topn(const DenseSource &src, int N, unsigned long long *sortbuf, Misc &ms) {
+__device__ __forceinline__ int dense_topn(const DenseSource &src, int N, unsigned long long *sortbuf, Misc &ms) {
     if (N <= 0) return 0;
     int total = 0;
     src.each([&](uint32_t, int, float) { ++total; });
@@ -830,7 +863,7 @@ __device__ int dense_topn(const DenseSource &src, int N, unsigned long long *sor
 // resolve top-k / top-p / the draw / top-N with radix selects over the whole row.
 // Taken when the chunk candidates cannot settle the row.
 template <typename TIn, int E>
-__device__ void dense_resolve(const Args &a, int row, const klsample_row_params &p, int mode,
+__device__ __forceinline__ void dense_resolve(const Args &a, int row, const klsample_row_params &p, int mode,
                               unsigned char *raw, Misc &ms) {
     constexpr int C = kThreads * E;
     const int V = a.V;
@@ -935,7 +968,7 @@ __device__ void dense_resolve(const Args &a, int row, const klsample_row_params 
 // Copy the entries of `src` scoring >= lo into the LDS list `dst` (capacity cap);
 // returns how many there were (the list holds min(count, cap) of them).
 template <typename Src>
-__device__ int gather_keys(const Src &src, float lo, unsigned long long *dst, int cap, Misc &ms) {
+__device__ __forceinline__ int gather_keys(const Src &src, float lo, unsigned long long *dst, int cap, Misc &ms) {
     if (threadIdx.x == 0) ms.ncand = 0;
     __syncthreads();
     src.each([&](uint32_t, int idx, float y) {
@@ -950,7 +983,7 @@ __device__ int gather_keys(const Src &src, float lo, unsigned long long *dst, in
 
 // Given D[0..n) sorted best first and the kept prefix length L, finish a sampled
 // row: normaliser, cut, top-N, inverse CDF in vocab order (D is reused as scratch).
-__device__ void finish_sampled(const Args &a, int row, int mode, const klsample_row_params &p,
+__device__ __forceinline__ void finish_sampled(const Args &a, int row, int mode, const klsample_row_params &p,
                                unsigned long long *D, int n, int L, double mref, Misc &ms) {
     const int V = a.V;
     RowOut r;
@@ -994,7 +1027,7 @@ __device__ void finish_sampled(const Args &a, int row, int mode, const klsample_
 // Length of the kept prefix of D[0..n) (sorted best first) under top-p: the first i
 // whose exclusive mass exceeds p * zref (the crossing entry is kept), or -1 if no
 // entry of D crosses.
-__device__ int topp_prefix(const unsigned long long *D, int n, double mref, double zref, float top_p, Misc &ms) {
+__device__ __forceinline__ int topp_prefix(const unsigned long long *D, int n, double mref, double zref, float top_p, Misc &ms) {
     const int seg = (n + kThreads - 1) / kThreads;
     const int i0 = min((int)threadIdx.x * seg, n), i1 = min(i0 + seg, n);
     double s = 0.0;
@@ -1012,22 +1045,249 @@ __device__ int topp_prefix(const unsigned long long *D, int n, double mref, doub
     return cut == 0x7fffffff ? -1 : cut;
 }
 
-// Resolve one row from its chunk summaries and candidates.  Runs in one workgroup
-// of kThreads.  Returns false when the candidates cannot settle the row (the caller
-// then runs dense_resolve).
+// ---------------------------------------------------------------------------------
+// One-wave finish of a row whose kept set is small: no barriers, one key per lane.
+
+// Bitonic sort of one 64-bit key per lane, ascending across the wave (~0 sorts last).
+__device__ __forceinline__ unsigned long long wave_sort(unsigned long long k) {
+    const int l = lane_id();
+#pragma unroll
+    for (int size = 2; size <= 64; size <<= 1) {
+#pragma unroll
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+            const uint32_t olo = (uint32_t)__shfl_xor((int)(uint32_t)k, stride);
+            const uint32_t ohi = (uint32_t)__shfl_xor((int)(uint32_t)(k >> 32), stride);
+            const unsigned long long o = ((unsigned long long)ohi << 32) | olo;
+            const bool keep_min = ((l & stride) == 0) == ((l & size) == 0);
+            k = keep_min ? (o < k ? o : k) : (o > k ? o : k);
+        }
+    }
+    return k;
+}
+
+// Sort D[0..n) ascending (best first) in LDS: one wave for n <= 64, else the block.
+__device__ __forceinline__ void sort_top(unsigned long long *D, int n) {
+    if (n <= 64) {
+        if (wave_id() == 0) {
+            const int l = lane_id();
+            unsigned long long k = l < n ? D[l] : ~0ull;
+            k = wave_sort(k);
+            if (l < n) D[l] = k;
+        }
+        __syncthreads();
+    } else {
+        sort_keys(D, n);
+    }
+}
+
+// Kept prefix of D[0..n) (sorted best first, n <= 64) under top-p: the first entry whose
+// exclusive mass exceeds p * zref is the last one kept.  Returns its count, or -1 if no
+// entry of D crosses.  Wave-uniform; call from one whole wave.
+__device__ __forceinline__ int wave_topp(const unsigned long long *D, int n, double mref, double zref, float top_p) {
+    const int l = lane_id();
+    const double w = l < n ? exp((double)desc_key_y(D[l]) - mref) : 0.0;
+    const double excl = wave_shift_excl(wave_incl_scan(w));
+    const unsigned long long cross = __ballot(l < n && excl > (double)top_p * zref);
+    return cross ? __ffsll((long long)cross) - 1 : -1;
+}
+
+// Row outputs from one wave: token, logprob, row state, and the top-N list taken from
+// D[0..count) (best first); count <= 64 and N <= 64.  Same contents as write_row.
+__device__ __forceinline__ void wave_write(const Args &a, int row, int mode, const RowOut &r,
+                                           const unsigned long long *D, int count) {
+    const int N = a.N, V = a.V;
+    const int l = lane_id();
+    if (N > 0) {
+        const int nv = min(N, V);
+        int32_t *ids = a.top_ids + (size_t)row * N;
+        float *lps = a.top_lp + (size_t)row * N;
+        const int idx = l < count ? desc_key_idx(D[l]) : -1;
+        if (l < count && l < nv) {
+            ids[l] = idx;
+            lps[l] = (float)((double)desc_key_y(D[l]) - (double)r.m - r.log_norm);
+        } else if (l >= nv && l < N) {
+            ids[l] = -1;
+            lps[l] = kNegInf;
+        }
+        if (count < nv) {
+            // fillers: the smallest ids not listed, all below 128 since count, nv <= 64
+            bool hit_lo = false, hit_hi = false;
+            for (int j = 0; j < count; ++j) {
+                const int ij = __builtin_amdgcn_readlane(idx, j);
+                hit_lo |= (ij == l);
+                hit_hi |= (ij == l + 64);
+            }
+            const unsigned long long free_lo = ~__ballot(hit_lo), free_hi = ~__ballot(hit_hi);
+            const unsigned long long below = (1ull << l) - 1ull;
+            const int need = nv - count;
+            const int r_lo = __popcll(free_lo & below);
+            if (((free_lo >> l) & 1ull) && r_lo < need) {
+                ids[count + r_lo] = l;
+                lps[count + r_lo] = kNegInf;
+            }
+            const int r_hi = __popcll(free_lo) + __popcll(free_hi & below);
+            if (((free_hi >> l) & 1ull) && r_hi < need) {
+                ids[count + r_hi] = l + 64;
+                lps[count + r_hi] = kNegInf;
+            }
+        }
+    }
+    if (l == 0) {
+        a.token[row] = r.token;
+        a.logprob[row] = (float)r.logprob;
+        klsample_row_info info;
+        info.max_score = r.m;
+        info.cut_score = r.cut;
+        info.cut_index = r.cut_idx;
+        info.kept = r.kept;
+        info.log_norm = r.log_norm;
+        info.path = r.path;
+        info.mode = mode;
+        a.rows[row] = info;
+        if (a.row_info) a.row_info[row] = info;
+    }
+}
+
+// Finish a sampled row in one wave: D[0..n) sorted best first, the first L kept
+// (1 <= L <= 64, L <= n), N <= 64.  Same results as finish_sampled.
+__device__ __forceinline__ void wave_finish(const Args &a, int row, int mode, const klsample_row_params &p,
+                                            const unsigned long long *D, int n, int L, double mref) {
+    const int l = lane_id();
+    const bool kept = l < L;
+    const float y = kept ? desc_key_y(D[l]) : kNegInf;
+    const int idx = kept ? desc_key_idx(D[l]) : 0x7fffffff;
+    const double w = kept ? exp((double)y - mref) : 0.0;
+    const double zf = wave_reduce(w, OpSumD(), 0.0);
+    RowOut r;
+    r.path = 0;
+    r.m = (float)mref;
+    r.cut = readlane(y, L - 1);
+    r.cut_idx = (L < n && desc_key_y(D[L]) == r.cut) ? __builtin_amdgcn_readlane(idx, L - 1) : a.V;
+    r.kept = L;
+    r.log_norm = log(zf);
+    // inverse CDF in vocab order: kept mass at indices <= this lane's index
+    double c = 0.0;
+    for (int j = 0; j < L; ++j) {
+        const int ij = __builtin_amdgcn_readlane(idx, j);
+        const double wj = readlane(w, j);
+        c += (ij <= idx) ? wj : 0.0;
+    }
+    const double target = (double)p.uniform * zf;
+    int tok = wave_reduce((kept && c > target) ? idx : 0x7fffffff, OpMinI(), 0x7fffffff);
+    if (tok == 0x7fffffff) tok = wave_reduce((kept && w > 0.0) ? idx : -1, OpMaxI(), -1);
+    const unsigned long long at = __ballot(kept && idx == tok);
+    const int lt = at ? __ffsll((long long)at) - 1 : 0;
+    r.token = __builtin_amdgcn_readlane(idx, lt);
+    r.logprob = (double)readlane(y, lt) - mref - r.log_norm;
+    wave_write(a, row, mode, r, D, min(a.N, L));
+}
+
+// ---------------------------------------------------------------------------------
+// The R best of A[0..n) (n > R >= 1) and every entry tied with the R-th, sorted best
+// first into D[0..cap).  Returns their count, or -1 if they do not fit.  One linear
+// 256-bin histogram over the entries' range [ylo, yhi] usually isolates them (the
+// bins above the R-th entry's bin, plus that bin); otherwise an exact radix select.
+__device__ __forceinline__ int select_top(const unsigned long long *A, int n, int R, float ylo, float yhi,
+                                          unsigned long long *D, int cap, Misc &ms) {
+    const double span = (double)yhi - (double)ylo;
+    int t = cap + 1;
+    if (span > 0.0) {
+        const double scale = 256.0 / span;
+        auto bin = [&](unsigned long long k) {
+            return min(255, (int)(((double)desc_key_y(k) - (double)ylo) * scale));
+        };
+        for (int i = threadIdx.x; i < 256; i += kThreads) ms.hist[i] = 0u;
+        __syncthreads();
+        for (int i = threadIdx.x; i < n; i += kThreads) atomicAdd(&ms.hist[bin(A[i])], 1u);
+        __syncthreads();
+        pick_digit_count(ms, (uint32_t)R);
+        const int b = (int)ms.sel_digit;
+        __syncthreads();
+        if (threadIdx.x == 0) ms.ncand = 0;
+        __syncthreads();
+        for (int i = threadIdx.x; i < n; i += kThreads) {
+            const unsigned long long k = A[i];
+            if (bin(k) >= b) {
+                const int pos = wave_append(&ms.ncand);
+                if (pos < cap) D[pos] = k;
+            }
+        }
+        __syncthreads();
+        t = ms.ncand;
+    }
+    if (t > cap) {
+        // the R-th entry's bin is crowded (or every entry is equal): exact radix select
+        const LdsSource src{A, n};
+        const float tau = fkey_inv(select_kth(src, (uint32_t)R, ms));
+        t = gather_keys(src, tau, D, cap, ms);
+        if (t > cap) return -1;
+    }
+    sort_top(D, t);
+    // keep the R best and the ties of the R-th
+    const float tau = desc_key_y(D[R - 1]);
+    int c = 0;
+    for (int i = R + (int)threadIdx.x; i < t; i += kThreads) c += (desc_key_y(D[i]) == tau) ? 1 : 0;
+    return R + block_sum(c, ms);
+}
+
+// Emit a row's outputs with its top-N list in D[0..count): one wave when the list is
+// short, else the block writer.
+__device__ __forceinline__ void emit_row(const Args &a, int row, int mode, const RowOut &r,
+                                         const unsigned long long *D, int count, Misc &ms) {
+    if (count <= 64 && a.N <= 64) {
+        if (wave_id() == 0) wave_write(a, row, mode, r, D, count);
+        return;
+    }
+    for (int t = threadIdx.x; t < count; t += kThreads) {
+        ms.topn_idx[t] = desc_key_idx(D[t]);
+        ms.topn_y[t] = desc_key_y(D[t]);
+    }
+    __syncthreads();
+    write_row(a, row, mode, r, count, ms);
+}
+
+constexpr int kSpecLoads = 8;    // candidate pairs each thread requests with the chunk summaries
+constexpr int kSpecPairs = 64;   // ... out of the first pairs of each chunk
+
+// Resolve one row from its chunk summaries and candidates.  Runs in one workgroup of
+// kThreads.  Returns false when the candidates cannot settle the row (the caller then
+// runs dense_resolve).
 template <typename TIn, int E>
-__device__ bool combine_row(const Args &a, int row, const klsample_row_params &p, int mode,
-                            unsigned char *raw, int *cnt, Misc &ms) {
+__device__ __forceinline__ bool combine_row(const Args &a, int row, const klsample_row_params &p, int mode,
+                                            unsigned char *raw, int *cnt, Misc &ms) {
     constexpr int C = kThreads * E;
     const int S = a.S, V = a.V, N = a.N;
     if ((a.options & KLSAMPLE_OPT_FORCE_DENSE) || S > kMaxChunksLds) return false;
+    const int tid = threadIdx.x;
     const ChunkStat *st = a.stats + (size_t)row * S;
+    const Cand *rc = a.cands + (size_t)row * S * a.cand_cap;
 
-    // chunk summaries: (max, lo, finite count, overflow) then (sum-exp, argmax), each
-    // reduced over the workgroup with one LDS exchange
+    // 1. The chunk summaries and the first candidate pairs of the first chunks, requested
+    //    together: one memory round trip for the common row.
+    const bool want_cands = !((mode == kGreedy || mode == kFull) && N == 0);
+    const int ppc = min(a.cand_cap / 2, kSpecPairs);   // a power of two
+    const int pshift = 31 - __clz(ppc);
+    const int nspec = want_cands ? min(S, (kSpecLoads * kThreads) >> pshift) : 0;
+    // (addresses are clamped into range rather than the loads predicated: a predicated
+    // load would be waited for before the next one is issued)
+    uint4 spec[kSpecLoads];
+#pragma unroll
+    for (int i = 0; i < kSpecLoads; ++i) {
+        const int q = tid + i * kThreads;
+        const int c = min(q >> pshift, max(nspec - 1, 0));
+        spec[i] = reinterpret_cast<const uint4 *>(rc + (size_t)c * a.cand_cap)[q & (ppc - 1)];
+    }
+    const bool has = tid < S;
+    const ChunkStat s0 = load_stat(st + min(tid, S - 1));
+
+    // 2. Row max, candidate bound, finite count, overflow; then sum-exp and argmax.
     float m = kNegInf, lo = kNegInf;
     int nfinite = 0, ovf = 0;
-    for (int c = threadIdx.x; c < S; c += kThreads) {
+    if (has) {
+        m = s0.m; lo = s0.y_thr; nfinite = s0.nfinite; ovf = s0.overflow;
+        cnt[tid] = min(s0.ncand, a.cand_cap);
+    }
+    for (int c = tid + kThreads; c < S; c += kThreads) {
         const ChunkStat s = st[c];
         m = fmaxf(m, s.m);
         lo = fmaxf(lo, s.y_thr);
@@ -1043,6 +1303,7 @@ __device__ bool combine_row(const Args &a, int row, const klsample_row_params &p
         ms.rf[0][wave_id()] = m; ms.rf[1][wave_id()] = lo;
         ms.ri[0][wave_id()] = nfinite; ms.ri[1][wave_id()] = ovf;
     }
+    if (tid == 0) { ms.ncand = 0; ms.ia = 0x7fffffff; ms.kmin = 0xffffffffu; ms.kmax = 0u; }
     __syncthreads();
     m = ms.rf[0][0]; lo = ms.rf[1][0]; nfinite = ms.ri[0][0]; ovf = ms.ri[1][0];
 #pragma unroll
@@ -1053,54 +1314,92 @@ __device__ bool combine_row(const Args &a, int row, const klsample_row_params &p
     if (ovf) return false;   // a chunk's candidates overflowed (massive ties)
     int arg = 0x7fffffff;
     double Z = 0.0;
-    for (int c = threadIdx.x; c < S; c += kThreads) {
-        const ChunkStat s = st[c];
-        if (mode == kGreedy && s.m == m) arg = min(arg, s.arg);
-        if (s.m > kNegInf) Z += s.z * exp((double)s.m - (double)m);
+    if (mode != kTopK) {
+        if (has) {
+            if (mode == kGreedy && s0.m == m) arg = s0.arg;
+            if (s0.m > kNegInf) Z += s0.z * exp((double)s0.m - (double)m);
+        }
+        for (int c = tid + kThreads; c < S; c += kThreads) {
+            const ChunkStat s = st[c];
+            if (mode == kGreedy && s.m == m) arg = min(arg, s.arg);
+            if (s.m > kNegInf) Z += s.z * exp((double)s.m - (double)m);
+        }
+    }
+
+    // 3. F = { candidates >= lo } into A; every element of the row scoring >= lo is in
+    //    it.  Its key range [ia, ib] is tracked for the selection.
+    unsigned long long *A = reinterpret_cast<unsigned long long *>(raw);
+    unsigned long long *D = A + kSortCap;
+    uint32_t kmin = 0xffffffffu, kmax = 0u;
+    auto take = [&](float y, int idx) {
+        const int pos = wave_append(&ms.ncand);
+        if (pos < kSortCap) A[pos] = desc_key(y, idx);
+        const uint32_t k = fkey(y);
+        kmin = min(kmin, k);
+        kmax = max(kmax, k);
+    };
+#pragma unroll
+    for (int i = 0; i < kSpecLoads; ++i) {
+        const int q = tid + i * kThreads;
+        const int c = q >> pshift;
+        if (c < nspec) {
+            const int nc = cnt[c], j = 2 * (q & (ppc - 1));
+            float y0 = __uint_as_float(spec[i].x), y1 = __uint_as_float(spec[i].z);
+            if (mode == kTopK) { y0 = __fdiv_rn(y0, p.temperature); y1 = __fdiv_rn(y1, p.temperature); }
+            if (j < nc && y0 >= lo) take(y0, (int)spec[i].y);
+            if (j + 1 < nc && y1 >= lo) take(y1, (int)spec[i].w);
+        }
+    }
+    if (want_cands) {
+        // the rest: chunks beyond the requested ones, and slots past the requested pairs
+        for (int c = wave_id(); c < S; c += kWaves) {
+            const int nc = cnt[c];
+            for (int j = (c < nspec ? 2 * ppc : 0) + lane_id(); j < nc; j += 64) {
+                const Cand cd = rc[(size_t)c * a.cand_cap + j];
+                const float y = (mode == kTopK) ? __fdiv_rn(cd.y, p.temperature) : cd.y;
+                if (y >= lo) take(y, cd.idx);
+            }
+        }
     }
     arg = wave_reduce(arg, OpMinI(), 0x7fffffff);
     Z = wave_reduce(Z, OpSumD(), 0.0);
+    kmin = wave_reduce(kmin, OpMinU(), 0xffffffffu);
+    kmax = wave_reduce(kmax, OpMaxU(), 0u);
+    if (lane_id() == 0) {
+        ms.red.d[wave_id()] = Z;
+        atomicMin(&ms.ia, arg);
+        atomicMin(&ms.kmin, kmin);
+        atomicMax(&ms.kmax, kmax);
+    }
     __syncthreads();
-    if (lane_id() == 0) { ms.ri[0][wave_id()] = arg; ms.red.d[wave_id()] = Z; }
-    __syncthreads();
-    arg = ms.ri[0][0]; Z = ms.red.d[0];
+    Z = ms.red.d[0];
 #pragma unroll
-    for (int w = 1; w < kWaves; ++w) { arg = min(arg, ms.ri[0][w]); Z += ms.red.d[w]; }
-
-    // F = { candidates >= lo }: every element of the row scoring >= lo is in it
-    unsigned long long *A = reinterpret_cast<unsigned long long *>(raw);
-    unsigned long long *D = A + kSortCap;
-    const CandSource src{a.cands + (size_t)row * S * a.cand_cap, cnt, S, a.cand_cap, lo};
-    int nF = gather_keys(src, lo, A, kSortCap, ms);
+    for (int w = 1; w < kWaves; ++w) Z += ms.red.d[w];
+    arg = ms.ia;
+    int nF = ms.ncand;
+    float ylo = fkey_inv(ms.kmin), yhi = fkey_inv(ms.kmax);
     if (nF > kSortCap) {
+        // too many candidates for LDS: narrow them to the best R with a radix select over
+        // the candidate slots
         const int R = (mode == kTopK) ? p.top_k : (mode == kTopP ? kThreads : N);
         if (R < 1 || R > kSortCap) return false;
-        const float lo2 = fkey_inv(select_kth(src, (uint32_t)R, ms));
-        nF = gather_keys(src, lo2, A, kSortCap, ms);
+        const CandSource src{rc, cnt, S, a.cand_cap, lo, mode == kTopK ? p.temperature : 0.f};
+        ylo = fkey_inv(select_kth(src, (uint32_t)R, ms));
+        nF = gather_keys(src, ylo, A, kSortCap, ms);
         if (nF > kSortCap) return false;
     }
-    const LdsSource fsrc{A, nF};
-    const bool small = nF <= kThreads;   // sort the candidates outright
-    if (small) rank_sort(A, nF);
+    // D[0..n) := the best R of F (ties with the R-th included), sorted best first
+    auto best = [&](int R) -> int {
+        if (R < nF) return select_top(A, nF, R, ylo, yhi, D, kSortCap, ms);
+        for (int i = tid; i < nF; i += kThreads) D[i] = A[i];
+        __syncthreads();
+        sort_top(D, nF);
+        return nF;
+    };
 
     if (mode == kGreedy || mode == kFull) {
-        int count = 0;
-        if (N > 0 && nF > 0) {
-            const int want = min(N, nF);
-            if (small) {
-                D = A;
-            } else {
-                const float tn = fkey_inv(select_kth(fsrc, (uint32_t)want, ms));
-                const int ng = gather_keys(fsrc, tn, D, kSortCap, ms);
-                sort_keys(D, ng);
-            }
-            count = want;
-            for (int t = threadIdx.x; t < count; t += kThreads) {
-                ms.topn_idx[t] = desc_key_idx(D[t]);
-                ms.topn_y[t] = desc_key_y(D[t]);
-            }
-            __syncthreads();
-        }
+        const int want = min(N, nF);
+        if (want > 0 && best(want) < 0) return false;
         RowOut r;
         r.path = 0;
         r.m = m;
@@ -1111,38 +1410,45 @@ __device__ bool combine_row(const Args &a, int row, const klsample_row_params &p
         if (mode == kGreedy) {
             r.token = (arg == 0x7fffffff) ? 0 : arg;
             r.logprob = -r.log_norm;
-        } else {
-            // chunk-level inverse CDF, then an ordered rescan of the chosen chunk
-            const double target = (double)p.uniform * Z;
-            int lastc;
-            double before;
-            int c = ordered_find(
-                S, [&](int i) { const ChunkStat s = st[i]; return s.m > kNegInf ? s.z * exp((double)s.m - (double)m) : 0.0; },
-                target, ms, lastc, before);
-            if (c < 0) { c = lastc >= 0 ? lastc : 0; }
-            const ChunkStat sc = st[c];
-            const int c0 = c * C, cn = min(C, V - c0);
-            const bool pen = has_penalty(a, p, row);
-            uint32_t *ctab = reinterpret_cast<uint32_t *>(raw);
-            __syncthreads();
-            if (pen) build_counts<C>(ctab, a, row, c0, cn);
-            const double scale = exp((double)sc.m - (double)m);
-            const double rem = (target - before) / scale;
-            int lastj;
-            double bj;
-            int j = ordered_find(
-                cn, [&](int i) {
-                    const float y = element_final<TIn>(a, p, row, c0 + i, pen ? ctab : nullptr, c0, true);
-                    return (double)exp_fast(y - sc.m);
-                },
-                rem, ms, lastj, bj);
-            if (j < 0) j = lastj >= 0 ? lastj : 0;
-            r.token = c0 + j;
-            const float yt = element_final<TIn>(a, p, row, r.token, pen ? ctab : nullptr, c0, true);
-            r.logprob = (double)yt - (double)m - r.log_norm;
-            __syncthreads();
+            emit_row(a, row, mode, r, D, want, ms);
+            return true;
         }
-        write_row(a, row, mode, r, count, ms);
+        // full distribution: chunk-level inverse CDF, then an ordered rescan of the
+        // chosen chunk (the top-N list moves out of the LDS the rescan reuses)
+        for (int t = tid; t < want; t += kThreads) {
+            ms.topn_idx[t] = desc_key_idx(D[t]);
+            ms.topn_y[t] = desc_key_y(D[t]);
+        }
+        __syncthreads();
+        const double target = (double)p.uniform * Z;
+        int lastc;
+        double before;
+        int c = ordered_find(
+            S, [&](int i) { const ChunkStat s = st[i]; return s.m > kNegInf ? s.z * exp((double)s.m - (double)m) : 0.0; },
+            target, ms, lastc, before);
+        if (c < 0) c = lastc >= 0 ? lastc : 0;
+        const ChunkStat sc = st[c];
+        const int c0 = c * C, cn = min(C, V - c0);
+        const bool pen = has_penalty(a, p, row);
+        uint32_t *ctab = reinterpret_cast<uint32_t *>(raw);
+        __syncthreads();
+        if (pen) build_counts<C>(ctab, a, row, c0, cn);
+        const double scale = exp((double)sc.m - (double)m);
+        const double rem = (target - before) / scale;
+        int lastj;
+        double bj;
+        int j = ordered_find(
+            cn, [&](int i) {
+                const float y = element_final<TIn>(a, p, row, c0 + i, pen ? ctab : nullptr, c0, true);
+                return (double)exp_fast(y - sc.m);
+            },
+            rem, ms, lastj, bj);
+        if (j < 0) j = lastj >= 0 ? lastj : 0;
+        r.token = c0 + j;
+        const float yt = element_final<TIn>(a, p, row, r.token, pen ? ctab : nullptr, c0, true);
+        r.logprob = (double)yt - (double)m - r.log_norm;
+        __syncthreads();
+        write_row(a, row, mode, r, want, ms);
         return true;
     }
 
@@ -1156,29 +1462,27 @@ __device__ bool combine_row(const Args &a, int row, const klsample_row_params &p
     }
 
     if (mode == kTopK) {
-        // top-k: every candidate >= the kk-th largest (ties included), sorted
-        const int kk = p.top_k;
-        int lk;
-        if (small) {
-            // A is sorted: the kept prefix runs to the last tie of the kk-th entry
-            D = A;
-            lk = nF;
-            if (nF > kk) {
-                const float tau = desc_key_y(A[kk - 1]);
-                int c = 0;
-                for (int i = kk + (int)threadIdx.x; i < nF; i += kThreads) c += (desc_key_y(A[i]) == tau) ? 1 : 0;
-                lk = kk + block_sum(c, ms);
-            }
-        } else {
-            const float tau = (nF > kk) ? fkey_inv(select_kth(fsrc, (uint32_t)kk, ms)) : kNegInf;
-            lk = gather_keys(fsrc, tau, D, kSortCap, ms);
-            sort_keys(D, lk);
-        }
+        // top-k: the kk best and every tie of the kk-th, then top-p on them
+        const int lk = best(p.top_k);
+        if (lk < 0) return false;
         const double mref = (double)desc_key_y(D[0]);
+        const bool topp = (p.flags & KLSAMPLE_ROW_TOP_P) != 0;
+        if (lk <= 64 && N <= 64) {
+            if (wave_id() == 0) {
+                int L = lk;
+                if (topp) {
+                    const double w = lane_id() < lk ? exp((double)desc_key_y(D[lane_id()]) - mref) : 0.0;
+                    const int cut = wave_topp(D, lk, mref, wave_reduce(w, OpSumD(), 0.0), p.top_p);
+                    if (cut > 0) L = cut;
+                }
+                wave_finish(a, row, mode, p, D, lk, L, mref);
+            }
+            return true;
+        }
         int L = lk;
-        if (p.flags & KLSAMPLE_ROW_TOP_P) {
+        if (topp) {
             double zs = 0.0;
-            for (int i = threadIdx.x; i < lk; i += kThreads) zs += exp((double)desc_key_y(D[i]) - mref);
+            for (int i = tid; i < lk; i += kThreads) zs += exp((double)desc_key_y(D[i]) - mref);
             const double zk = block_sumd(zs, ms);
             const int cut = topp_prefix(D, lk, mref, zk, p.top_p, ms);
             if (cut > 0) L = cut;
@@ -1187,34 +1491,32 @@ __device__ bool combine_row(const Args &a, int row, const klsample_row_params &p
         return true;
     }
 
-    // top-p alone: walk the best kThreads first, then every candidate
+    // top-p alone: the best 64 (one wave), then the best 256, then every candidate
     const double mref = (double)m;
     int n = 0, L = -1;
-    if (small) {
-        D = A;
-        n = nF;
-        L = topp_prefix(D, n, mref, Z, p.top_p, ms);
-        if (L < 0) {
-            if (lo > kNegInf) return false;
-            L = n;
+    for (int R = 64;; R = (R < kThreads) ? kThreads : nF) {
+        if (R > nF) R = nF;
+        n = best(R);
+        if (n < 0) return false;
+        if (n <= 64) {
+            if (wave_id() == 0) {
+                const int cut = wave_topp(D, n, mref, Z, p.top_p);
+                if (lane_id() == 0) ms.flag = cut;
+            }
+            __syncthreads();
+            L = ms.flag;
+        } else {
+            L = topp_prefix(D, n, mref, Z, p.top_p, ms);
         }
-        finish_sampled(a, row, mode, p, D, n, L, mref, ms);
-        return true;
+        if (L > 0 || R >= nF) break;
     }
-    const float t256 = fkey_inv(select_kth(fsrc, (uint32_t)kThreads, ms));
-    n = gather_keys(fsrc, t256, D, kSortCap, ms);
-    sort_keys(D, n);
-    L = topp_prefix(D, n, mref, Z, p.top_p, ms);
     if (L < 0) {
-        for (int i = threadIdx.x; i < nF; i += kThreads) D[i] = A[i];
-        __syncthreads();
-        n = nF;
-        sort_keys(D, n);
-        L = topp_prefix(D, n, mref, Z, p.top_p, ms);
-        if (L < 0) {
-            if (lo > kNegInf) return false;   // the kept mass reaches past the candidates
-            L = n;                            // the candidates are the whole row
-        }
+        if (lo > kNegInf) return false;   // the kept mass reaches past the candidates
+        L = n;                            // the candidates are the whole row
+    }
+    if (L <= 64 && N <= 64) {
+        if (wave_id() == 0) wave_finish(a, row, mode, p, D, n, L, mref);
+        return true;
     }
     finish_sampled(a, row, mode, p, D, n, L, mref, ms);
     return true;
@@ -1234,29 +1536,41 @@ __device__ __forceinline__ void map_block(const Args &a, int &row, int &chunk) {
     }
 }
 
-template <int C>
+// LDS of the streaming pass.  Penalty phase: the chunk's history counts (16 bits, two
+// per word), the list of distinct history elements of the chunk and, per thread, a
+// mask of its register slots holding one.  Bound phase (later): the group-maximum
+// keys.  The two phases never overlap.
+constexpr int kHitCap = 2 * kThreads;   // distinct history elements per chunk on the list path
+
+template <int E>
 struct ScanLds {
-    static constexpr int a = C * 4;
-    static constexpr int b = kMaxGroupKeys * 4;
-    static constexpr int value = a > b ? a : b;
+    static constexpr int C = kThreads * E;
+    static constexpr int counts = C * 2;
+    static constexpr int hits_off = counts;
+    static constexpr int mask_off = hits_off + kHitCap * 2;
+    static constexpr int penalty = mask_off + kThreads * 4;
+    static constexpr int keys = kThreads * (E < 16 ? E : 16) * 4;
+    static constexpr int value = penalty > keys ? penalty : keys;
 };
 
-template <int C>
-struct RowLds {
-    static constexpr int a = C * 4;
-    static constexpr int b = 2 * kSortCap * 8;
-    static constexpr int value = a > b ? a : b;
-};
-
-// Streaming pass: one workgroup per (row, chunk).  At least four waves per SIMD must
-// fit: that is what the LDS footprint of the largest chunk allows anyway.
+// Streaming pass: one workgroup per (row, chunk).  The LDS footprint (at most ~19 KB)
+// lets eight workgroups share a CU; the register budget is capped so that five
+// (32 elements per thread) or eight waves per SIMD fit, to hide HBM latency.
+//
+// Penalties: the row's history ids are counted into an LDS table; the first thread
+// to count an element lists it, marks it in its owner's slot mask, and later applies
+// the penalty to it alone (one element per thread).  The owners replace listed
+// elements by -inf in their registers, so the dense work (bound, candidates, sums)
+// needs no per-element branch; the listed elements join the sums and the candidates
+// separately.  The bound over the remaining elements stays a valid lower bound.
 template <typename TIn, int E>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) void scan_kernel(Args a) {
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(E >= 32 ? 4 : 8))) void scan_kernel(Args a) {
     constexpr int VW = Loader<TIn>::VW;
     constexpr int NV = E / VW;
     constexpr int C = kThreads * E;
-    __shared__ __attribute__((aligned(16))) unsigned char raw[ScanLds<C>::value];
-    __shared__ Misc ms;
+    constexpr int kHitsPer = kHitCap / kThreads;
+    __shared__ __attribute__((aligned(16))) unsigned char raw[ScanLds<E>::value];
+    __shared__ ScanMisc ms;
 
     int row, chunk;
     map_block(a, row, chunk);
@@ -1264,10 +1578,36 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
     const int V = a.V;
     const int tid = threadIdx.x;
     const int mode = row_mode(p, V);
+    const bool divided = (mode == kTopP || mode == kFull);   // scores stream in final space
     const int c0 = chunk * C;
     const int cn = min(C, V - c0);
     const TIn *src = reinterpret_cast<const TIn *>(a.logits) + (int64_t)row * a.row_stride + c0;
-    if (tid == 0) ms.ncand = 0;
+    if (tid == 0) { ms.ncand = 0; ms.nhits = 0; }
+
+    // History of a penalised row.  Its first ids are requested before the logits, so
+    // the count table is built while the logits are in flight.  Counts are 16-bit
+    // halves of LDS words (exact below 65536 ids); longer histories take the 32-bit
+    // path below.
+    int h0 = 0, h1 = 0;
+    if ((p.flags & (KLSAMPLE_ROW_REPETITION | KLSAMPLE_ROW_PRESENCE_FREQUENCY)) && a.hist_off != nullptr) {
+        h0 = a.hist_off[row];
+        h1 = a.hist_off[row + 1];
+    }
+    const int H = h1 - h0;
+    const bool packed = H > 0 && H < 65536;
+    uint32_t *tab = reinterpret_cast<uint32_t *>(raw);
+    uint16_t *hits = reinterpret_cast<uint16_t *>(raw + ScanLds<E>::hits_off);
+    uint32_t *hmask = reinterpret_cast<uint32_t *>(raw + ScanLds<E>::mask_off);
+    int hid[8];
+    if (packed) {
+        // clamped addresses, unpredicated loads: all eight stay in flight together
+#pragma unroll
+        for (int j = 0; j < 8; ++j) hid[j] = a.hist_ids[min(h0 + tid + j * kThreads, h1 - 1)];
+        uint4 *t4 = reinterpret_cast<uint4 *>(raw);
+#pragma unroll
+        for (int i = tid; i < C / 8; i += kThreads) t4[i] = make_uint4(0u, 0u, 0u, 0u);
+        hmask[tid] = 0u;
+    }
 
     float x[E];
     if (cn == C && a.vec_ok) {
@@ -1285,21 +1625,107 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
         }
     }
 
-    if (has_penalty(a, p, row)) {
-        uint32_t *cnt = reinterpret_cast<uint32_t *>(raw);
-        build_counts<C>(cnt, a, row, c0, cn);
+    // penalised scores of this thread's listed history elements (-inf: none)
+    float hy[kHitsPer];
+    int hix[kHitsPer];
 #pragma unroll
-        for (int v = 0; v < NV; ++v) {
-            const int li = (v * kThreads + tid) * VW;
-#pragma unroll
-            for (int e = 0; e < VW; ++e) {
-                const uint32_t c = cnt[li + e];
-                if (c) x[v * VW + e] = penalize(x[v * VW + e], c, p);
+    for (int j = 0; j < kHitsPer; ++j) { hy[j] = kNegInf; hix[j] = 0; }
+
+    if (packed) {
+        __syncthreads();   // table cleared
+        // (the ids were loaded from clamped positions: h >= h1 marks a repeat, not an id)
+        auto count = [&](int id, int h) {
+            const unsigned rel = (unsigned)(id - c0);
+            if (h < h1 && id >= 0 && rel < (unsigned)cn) {
+                const uint32_t sh = (rel & 1u) * 16u;
+                const uint32_t old = atomicAdd(&tab[rel >> 1], 1u << sh);
+                if (((old >> sh) & 0xffffu) == 0u) {
+                    // first count of this element: list it, mark its owner's slot
+                    const int pos = atomicAdd(&ms.nhits, 1);
+                    if (pos < kHitCap) hits[pos] = (uint16_t)rel;
+                    const unsigned owner = (rel / VW) % kThreads;
+                    const unsigned slot = (rel / (VW * kThreads)) * VW + rel % VW;
+                    atomicOr(&hmask[owner], 1u << slot);
+                }
             }
+        };
+#pragma unroll
+        for (int j = 0; j < 8; ++j) count(hid[j], h0 + tid + j * kThreads);
+        for (int hb = h0 + tid + 8 * kThreads; hb < h1; hb += 8 * kThreads) {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) hid[j] = a.hist_ids[min(hb + j * kThreads, h1 - 1)];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) count(hid[j], hb + j * kThreads);
         }
         __syncthreads();
+        const int nh = ms.nhits;
+        if (nh <= kHitCap) {
+            // listed elements: original logit re-read (cached), penalty, temperature
+#pragma unroll
+            for (int j = 0; j < kHitsPer; ++j) {
+                const int k = tid + j * kThreads;
+                if (k < nh) {
+                    const int rel = hits[k];
+                    const uint32_t c = (tab[rel >> 1] >> ((rel & 1) * 16)) & 0xffffu;
+                    float y = penalize(Loader<TIn>::one(src + rel), c, p);
+                    if (divided) y = __fdiv_rn(y, p.temperature);
+                    hy[j] = y;
+                    hix[j] = rel;
+                }
+            }
+            // owners drop their listed elements from the dense work
+            const uint32_t mk = hmask[tid];
+#pragma unroll
+            for (int e = 0; e < E; ++e) x[e] = ((mk >> e) & 1u) ? kNegInf : x[e];
+        } else {
+            // more distinct history elements than the list holds: per-element penalties
+#pragma unroll
+            for (int v = 0; v < NV; ++v) {
+                const int li = (v * kThreads + tid) * VW;   // even: element pairs share words
+                uint32_t w[VW / 2];
+                if constexpr (VW == 4) {
+                    const uint2 q = *reinterpret_cast<const uint2 *>(&tab[li >> 1]);
+                    w[0] = q.x; w[1] = q.y;
+                } else {
+                    const uint4 q = *reinterpret_cast<const uint4 *>(&tab[li >> 1]);
+                    w[0] = q.x; w[1] = q.y; w[2] = q.z; w[3] = q.w;
+                }
+#pragma unroll
+                for (int e = 0; e < VW; ++e) {
+                    const uint32_t c = (w[e >> 1] >> ((e & 1) * 16)) & 0xffffu;
+                    if (c) x[v * VW + e] = penalize(x[v * VW + e], c, p);
+                }
+            }
+        }
+        __syncthreads();   // the table area is reused for the bound's keys
+    } else if (H > 0) {
+        // 32-bit counts over slices of the chunk that fit the table
+        constexpr int RC = ScanLds<E>::value / 4;
+        for (int r0 = 0; r0 < cn; r0 += RC) {
+            for (int i = tid; i < RC; i += kThreads) tab[i] = 0u;
+            __syncthreads();
+            const int lim = min(RC, cn - r0);
+            for (int h = h0 + tid; h < h1; h += kThreads) {
+                const int id = a.hist_ids[h];
+                const unsigned rel = (unsigned)(id - c0 - r0);
+                if (id >= 0 && rel < (unsigned)lim) atomicAdd(&tab[rel], 1u);
+            }
+            __syncthreads();
+#pragma unroll
+            for (int v = 0; v < NV; ++v) {
+#pragma unroll
+                for (int e = 0; e < VW; ++e) {
+                    const unsigned rel = (unsigned)((v * kThreads + tid) * VW + e - r0);
+                    if (rel < (unsigned)RC) {
+                        const uint32_t c = tab[rel];
+                        if (c) x[v * VW + e] = penalize(x[v * VW + e], c, p);
+                    }
+                }
+            }
+            __syncthreads();
+        }
     }
-    if (mode == kTopP || mode == kFull) {
+    if (divided) {
 #pragma unroll
         for (int e = 0; e < E; ++e) x[e] = __fdiv_rn(x[e], p.temperature);
     }
@@ -1316,6 +1742,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
         float mt = kNegInf;
 #pragma unroll
         for (int e = 0; e < E; ++e) mt = fmaxf(mt, x[e]);
+#pragma unroll
+        for (int j = 0; j < kHitsPer; ++j) mt = fmaxf(mt, hy[j]);
         const float m = block_max(mt, ms);
         if (mode == kGreedy) {
             int at = 0x7fffffff;
@@ -1326,6 +1754,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
                 for (int e = 0; e < VW; ++e)
                     if (x[v * VW + e] == m && li + e < cn && li + e < at) at = li + e;
             }
+#pragma unroll
+            for (int j = 0; j < kHitsPer; ++j)
+                if (hy[j] == m && hix[j] < at) at = hix[j];
             at = block_min(at, ms);
             st.arg = (at == 0x7fffffff) ? 0x7fffffff : c0 + at;
         }
@@ -1337,6 +1768,11 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
                 z += (double)exp_fast(x[e] - m);
                 nfin += (x[e] > kNegInf) ? 1 : 0;
             }
+#pragma unroll
+            for (int j = 0; j < kHitsPer; ++j) {
+                z += (double)exp_fast(hy[j] - m);
+                nfin += (hy[j] > kNegInf) ? 1 : 0;
+            }
         }
         st.z = block_sumd(z, ms);
         st.nfinite = block_sum(nfin, ms);
@@ -1347,36 +1783,45 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
                   : (mode == kTopK ? p.top_k : max(kTopPCandidates, a.N));
     if (K > 0) {
         float bound = kNegInf;
-        if (K < cn) bound = chunk_bound<E>(x, K, reinterpret_cast<uint32_t *>(raw), ms);
+        if (K < cn) bound = chunk_bound<E>(x, K, tab, ms);
         else __syncthreads();
-        float thr = bound;
-        if (mode == kTopK && bound > kNegInf) {
-            // widen by 8 ulps so every element whose quotient by T rounds to at least
-            // bound / T is kept
-            const float d = fmaxf(fabsf(bound) * 9.5367431640625e-07f, p.temperature * 7.174648137343064e-43f);
-            thr = bound - d;
+        // candidates: elements >= thr; a finite threshold also excludes -inf scores
+        float thr = -__FLT_MAX__;
+        if (bound > kNegInf) {
+            thr = bound;
+            if (mode == kTopK) {
+                // widen by 8 ulps so every element whose quotient by T rounds to at
+                // least bound / T is kept
+                const float d = fmaxf(fabsf(bound) * 9.5367431640625e-07f, p.temperature * 7.174648137343064e-43f);
+                thr = bound - d;
+            }
         }
         st.y_thr = (mode == kTopK) ? (bound > kNegInf ? __fdiv_rn(bound, p.temperature) : kNegInf) : bound;
         int my = 0;
 #pragma unroll
-        for (int e = 0; e < E; ++e) my += (x[e] >= thr && x[e] > kNegInf) ? 1 : 0;
+        for (int e = 0; e < E; ++e) my += (x[e] >= thr) ? 1 : 0;
+#pragma unroll
+        for (int j = 0; j < kHitsPer; ++j) my += (hy[j] >= thr) ? 1 : 0;
         const int incl = wave_incl_scan(my);
         const int wtot = readlane(incl, 63);
         int wbase = 0;
         if (lane_id() == 0 && wtot > 0) wbase = atomicAdd(&ms.ncand, wtot);
         wbase = readlane(wbase, 0);
         int pos = wbase + incl - my;
+        // scores are written as streamed: top-k rows in the penalised space (the row
+        // kernel divides by T), the others in final space
         Cand *out = a.cands + ((size_t)row * a.S + chunk) * a.cand_cap;
+        const int cap = a.cand_cap;
 #pragma unroll
         for (int v = 0; v < NV; ++v) {
             const int li = (v * kThreads + tid) * VW;
 #pragma unroll
             for (int e = 0; e < VW; ++e) {
                 const float xv = x[v * VW + e];
-                if (xv >= thr && xv > kNegInf) {
-                    if (pos < a.cand_cap) {
+                if (xv >= thr) {
+                    if (pos < cap) {
                         Cand cd;
-                        cd.y = (mode == kTopK) ? __fdiv_rn(xv, p.temperature) : xv;
+                        cd.y = xv;
                         cd.idx = c0 + li + e;
                         out[pos] = cd;
                     }
@@ -1384,12 +1829,31 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) v
                 }
             }
         }
+#pragma unroll
+        for (int j = 0; j < kHitsPer; ++j) {
+            if (hy[j] >= thr) {
+                if (pos < cap) {
+                    Cand cd;
+                    cd.y = hy[j];
+                    cd.idx = c0 + hix[j];
+                    out[pos] = cd;
+                }
+                ++pos;
+            }
+        }
         __syncthreads();
-        st.ncand = min(ms.ncand, a.cand_cap);
-        st.overflow = ms.ncand > a.cand_cap ? 1 : 0;
+        st.ncand = min(ms.ncand, cap);
+        st.overflow = ms.ncand > cap ? 1 : 0;
     }
     if (tid == 0) a.stats[(size_t)row * a.S + chunk] = st;
 }
+
+template <int C>
+struct RowLds {
+    static constexpr int a = C * 4;
+    static constexpr int b = 2 * kSortCap * 8;
+    static constexpr int value = a > b ? a : b;
+};
 
 // One workgroup per row: combine the chunk candidates, or run the multi-pass path.
 template <typename TIn, int E>

@@ -95,3 +95,29 @@ def test_engine_style_loop_runs_unchanged():
             assert res.stopped
         return generated
     assert asyncio.run(main()) == {f'r{i}': [2, 2] for i in range(3)}
+
+
+def test_integration_ctypes_stub_matches_the_drop_in():
+    """The raw ctypes binding shown in INTEGRATION.md runs as written and returns the
+    drop-in's tokens and logprobs."""
+    import re
+    from pathlib import Path
+
+    from klsample import _lib, workloads
+    from klsample.runner import runner_for
+
+    root = Path(__file__).resolve().parents[1]
+    blocks = re.findall(r'```python\n(.*?)```', (root / 'INTEGRATION.md').read_text(), re.S)
+    stub = next(b for b in blocks if 'klsample_run' in b)
+    stub = stub.replace('/path/to/repo/gpu-kernel-lab_amd/klsample/libklsample.so', str(_lib.LIBRARY))
+    ns = {}
+    exec(compile(stub, 'INTEGRATION.md', 'exec'), ns)
+    w = workloads.make('cpu_reference_b8', num_logprobs=3)
+    hist = [[5, 9, -1]] * w.batch
+    params = [SamplingParams(p.temperature, p.top_k, p.top_p, 1.2, p.stop_token_ids, p.seed, 3) for p in w.params]
+    logits = w.logits.cuda()
+    tok, lp, top_ids, top_lp = ns['sample_rows'](logits, params, hist, w.uniforms, 3)
+    want = runner_for(logits.device).run(logits, params, hist, w.uniforms, 3)
+    assert np.array_equal(tok.numpy(), want.tokens)
+    assert np.array_equal(lp.numpy(), want.logprobs)
+    assert np.array_equal(top_ids.numpy(), want.top_ids)
