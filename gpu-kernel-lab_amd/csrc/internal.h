@@ -14,7 +14,6 @@ constexpr int kWaves = kThreads / 64;
 constexpr int kSortCap = 2048;         // candidates a row can resolve in LDS
 constexpr int kTopPCandidates = 64;    // per-chunk candidates for rows with top-p but no top-k
 constexpr int kMaxLogprobs = 256;      // largest supported num_logprobs
-constexpr int kMaxGroupKeys = 4096;    // group maxima examined per chunk
 constexpr int kMaxBatch = 65536;       // rows per call
 constexpr int kMaxChunksLds = 4096;    // chunks per row the candidate combine indexes in LDS
 

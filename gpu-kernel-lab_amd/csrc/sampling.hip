@@ -102,6 +102,7 @@ struct Red {
 // The streaming pass needs little beyond the reductions (its LDS footprint sets how
 // many workgroups share a CU).
 struct ScanMisc : Red {
+    uint32_t wbound[kWaves];
     uint32_t bound_key;
     int ncand;
     int nhits;
@@ -322,14 +323,55 @@ __device__ __forceinline__ float element_final(const Args &a, const klsample_row
 }
 
 // ---------------------------------------------------------------------------------
-// Bound on the chunk's K-th largest value: the K-th largest of the maxima of
-// kThreads*G disjoint groups (E/G consecutive register elements per group).  K groups
-// have a maximum at or above it, so at least K elements are.
+// Lower bound on a chunk's K-th largest value.  Each wave takes the Kw-th largest
+// (Kw = ceil(K / 4)) of the maxima of 64*G disjoint groups of its own elements (E/G
+// consecutive register elements per group): Kw group maxima, hence Kw elements, are at
+// or above it.  The chunk bound is the smallest of the four waves' values, so each
+// wave has Kw elements at or above it, K in all.  The waves search in parallel, by
+// bisection over order-preserving keys with ballots, without barriers.
+
+// Kw-th largest group-maximum key of the calling wave (low 8 key bits zero, so it may
+// sit up to 2^-15 relative below the exact value).  Wave-uniform.
 template <int E, int G>
-__device__ __forceinline__ float group_bound(const float (&x)[E], int K, uint32_t *keys, ScanMisc &ms) {
+__device__ __forceinline__ uint32_t wave_group_bound(const float (&x)[E], int Kw) {
     constexpr int GS = E / G;
-    constexpr int NG = kThreads * G;
-    constexpr int PER = NG / 64;   // keys per lane of the counting wave
+    uint32_t k[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        float mx = kNegInf;
+#pragma unroll
+        for (int j = 0; j < GS; ++j) mx = fmaxf(mx, x[g * GS + j]);
+        k[g] = fkey(mx);
+    }
+    uint32_t t = 0u;
+    for (int bit = 31; bit >= 8; --bit) {
+        const uint32_t cand = t | (1u << bit);
+        int c = 0;
+#pragma unroll
+        for (int g = 0; g < G; ++g) c += __popcll(__ballot(k[g] >= cand));
+        if (c >= Kw) t = cand;
+    }
+    return t;
+}
+
+template <int E>
+__device__ __forceinline__ uint32_t wave_group_bound_dispatch(const float (&x)[E], int G, int Kw) {
+    switch (G) {
+        case 1: return wave_group_bound<E, 1>(x, Kw);
+        case 2: if constexpr (E >= 2) return wave_group_bound<E, 2>(x, Kw); break;
+        case 4: if constexpr (E >= 4) return wave_group_bound<E, 4>(x, Kw); break;
+        case 8: if constexpr (E >= 8) return wave_group_bound<E, 8>(x, Kw); break;
+        default: if constexpr (E >= 16) return wave_group_bound<E, 16>(x, Kw); break;
+    }
+    return 0u;
+}
+
+// Block-wide fallback: the K-th largest of the maxima of kThreads*G disjoint groups
+// (E/G consecutive register elements per group), by one wave over keys in LDS.
+template <int E, int G>
+__device__ __forceinline__ float block_group_bound(const float (&x)[E], int K, uint32_t *keys, ScanMisc &ms) {
+    constexpr int GS = E / G;
+    constexpr int PER = kThreads * G / 64;   // keys per lane of the counting wave
 #pragma unroll
     for (int g = 0; g < G; ++g) {
         float mx = kNegInf;
@@ -339,68 +381,72 @@ __device__ __forceinline__ float group_bound(const float (&x)[E], int K, uint32_
     }
     __syncthreads();
     if (wave_id() == 0) {
-        // largest t with #{keys >= t} >= K, bit by bit from the top; counts are wave
-        // ballots, so each step is a compare and a scalar popcount per key slot
         const int lane = lane_id();
         uint32_t t = 0u;
-        if constexpr (PER <= 4) {
-            uint32_t k[PER];
-#pragma unroll
-            for (int j = 0; j < PER; ++j) k[j] = keys[j * 64 + lane];
-            // the low 8 key bits stay zero: the bound sits at most 2^-15 (relative)
-            // below the exact K-th group maximum, a handful of extra candidates
-            for (int bit = 31; bit >= 8; --bit) {
-                const uint32_t cand = t | (1u << bit);
-                int c = 0;
-#pragma unroll
-                for (int j = 0; j < PER; ++j) c += __popcll(__ballot(k[j] >= cand));
-                if (c >= K) t = cand;
-            }
-        } else {
-            // many keys per lane: re-read them from LDS every step (volatile keeps the
-            // compiler from hoisting all of them into registers for the whole kernel)
-            const volatile uint32_t *vk = keys;
+        // re-read the keys every step (volatile keeps the compiler from hoisting all
+        // of them into registers for the whole kernel)
+        const volatile uint32_t *vk = keys;
 #pragma unroll 1
-            for (int bit = 31; bit >= 8; --bit) {
-                const uint32_t cand = t | (1u << bit);
-                int c = 0;
+        for (int bit = 31; bit >= 8; --bit) {
+            const uint32_t cand = t | (1u << bit);
+            int c = 0;
 #pragma unroll 4
-                for (int j = 0; j < PER; ++j) c += __popcll(__ballot(vk[j * 64 + lane] >= cand));
-                if (c >= K) t = cand;
-            }
+            for (int j = 0; j < PER; ++j) c += __popcll(__ballot(vk[j * 64 + lane] >= cand));
+            if (c >= K) t = cand;
         }
         if (lane == 0) ms.bound_key = t;
     }
     __syncthreads();
-    // keys below that of -FLT_MAX stand for -inf (groups without a finite element)
     return ms.bound_key < 0x00800000u ? kNegInf : fkey_inv(ms.bound_key);
 }
 
 template <int E>
-__device__ __forceinline__ float group_bound_dispatch(const float (&x)[E], int G, int K, uint32_t *keys, ScanMisc &ms) {
+__device__ __forceinline__ float block_group_bound_dispatch(const float (&x)[E], int G, int K, uint32_t *keys,
+                                                            ScanMisc &ms) {
     switch (G) {
-        case 1: return group_bound<E, 1>(x, K, keys, ms);
-        case 2: if constexpr (E >= 2) return group_bound<E, 2>(x, K, keys, ms); break;
-        case 4: if constexpr (E >= 4) return group_bound<E, 4>(x, K, keys, ms); break;
-        case 8: if constexpr (E >= 8) return group_bound<E, 8>(x, K, keys, ms); break;
-        default: if constexpr (E >= 16) return group_bound<E, 16>(x, K, keys, ms); break;
+        case 1: return block_group_bound<E, 1>(x, K, keys, ms);
+        case 2: if constexpr (E >= 2) return block_group_bound<E, 2>(x, K, keys, ms); break;
+        case 4: if constexpr (E >= 4) return block_group_bound<E, 4>(x, K, keys, ms); break;
+        case 8: if constexpr (E >= 8) return block_group_bound<E, 8>(x, K, keys, ms); break;
+        default: if constexpr (E >= 16) return block_group_bound<E, 16>(x, K, keys, ms); break;
     }
     return kNegInf;
 }
 
-// Lower bound on the chunk's K-th largest element (-inf: keep every element).  Groups
-// start as coarse as 4K groups allow and are refined while fewer than K of them hold a
-// finite element (a partial last chunk, masked logits).
+// The chunk bound (-inf: keep every element).  Full chunks take the per-wave bound:
+// groups start as coarse as 4*Kw groups per wave allow and a wave refines them while
+// fewer than Kw hold a finite element.  A partial chunk, or a wave still short of Kw
+// finite groups (masked or massively tied scores), takes one bound over the whole
+// chunk instead.  `keys` holds kThreads * min(E, 16) words of LDS.  Ends with a barrier.
 template <int E>
-__device__ __forceinline__ float chunk_bound(const float (&x)[E], int K, uint32_t *keys, ScanMisc &ms) {
-    constexpr int kMaxG = (E < kMaxGroupKeys / kThreads) ? E : kMaxGroupKeys / kThreads;
+__device__ __forceinline__ float chunk_bound(const float (&x)[E], int K, int cn, uint32_t *keys, ScanMisc &ms) {
+    constexpr int kMaxG = E < 16 ? E : 16;
+    constexpr int C = kThreads * E;
+    const int Kw = (K + kWaves - 1) / kWaves;
+    uint32_t t = 0u;
+    if (cn == C && Kw <= 64 * kMaxG) {
+        int G = 1;
+        while (G < kMaxG && 64 * G < 4 * Kw) G <<= 1;
+        t = wave_group_bound_dispatch<E>(x, G, Kw);
+        while (t < 0x00800000u && G < kMaxG) {
+            G <<= 1;
+            t = wave_group_bound_dispatch<E>(x, G, Kw);
+        }
+    }
+    if (lane_id() == 0) ms.wbound[wave_id()] = t;
+    __syncthreads();
+    uint32_t b = ms.wbound[0];
+#pragma unroll
+    for (int w = 1; w < kWaves; ++w) b = min(b, ms.wbound[w]);
+    // keys below that of -FLT_MAX stand for -inf (groups without a finite element)
+    if (b >= 0x00800000u) return fkey_inv(b);
+    if (K > kThreads * kMaxG) return kNegInf;
     int G = 1;
     while (G < kMaxG && G * kThreads < 4 * K) G <<= 1;
-    if (K > G * kThreads) return kNegInf;
-    float bound = group_bound_dispatch<E>(x, G, K, keys, ms);
+    float bound = block_group_bound_dispatch<E>(x, G, K, keys, ms);
     while (bound == kNegInf && G < kMaxG) {
         G <<= 1;
-        bound = group_bound_dispatch<E>(x, G, K, keys, ms);
+        bound = block_group_bound_dispatch<E>(x, G, K, keys, ms);
     }
     return bound;
 }
@@ -1538,8 +1584,7 @@ __device__ __forceinline__ void map_block(const Args &a, int &row, int &chunk) {
 
 // LDS of the streaming pass.  Penalty phase: the chunk's history counts (16 bits, two
 // per word), the list of distinct history elements of the chunk and, per thread, a
-// mask of its register slots holding one.  Bound phase (later): the group-maximum
-// keys.  The two phases never overlap.
+// mask of its register slots holding one.  Later, the fallback bound's group keys.
 constexpr int kHitCap = 2 * kThreads;   // distinct history elements per chunk on the list path
 
 template <int E>
@@ -1549,7 +1594,7 @@ struct ScanLds {
     static constexpr int hits_off = counts;
     static constexpr int mask_off = hits_off + kHitCap * 2;
     static constexpr int penalty = mask_off + kThreads * 4;
-    static constexpr int keys = kThreads * (E < 16 ? E : 16) * 4;
+    static constexpr int keys = kThreads * (E < 16 ? E : 16) * 4;   // fallback bound (later)
     static constexpr int value = penalty > keys ? penalty : keys;
 };
 
@@ -1564,7 +1609,7 @@ struct ScanLds {
 // needs no per-element branch; the listed elements join the sums and the candidates
 // separately.  The bound over the remaining elements stays a valid lower bound.
 template <typename TIn, int E>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(E >= 32 ? 4 : 8))) void scan_kernel(Args a) {
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(E >= 32 ? 4 : (E >= 16 && sizeof(TIn) == 2) ? 7 : 8))) void scan_kernel(Args a) {
     constexpr int VW = Loader<TIn>::VW;
     constexpr int NV = E / VW;
     constexpr int C = kThreads * E;
@@ -1697,7 +1742,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(E >= 3
                 }
             }
         }
-        __syncthreads();   // the table area is reused for the bound's keys
+        __syncthreads();
     } else if (H > 0) {
         // 32-bit counts over slices of the chunk that fit the table
         constexpr int RC = ScanLds<E>::value / 4;
@@ -1783,7 +1828,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(E >= 3
                   : (mode == kTopK ? p.top_k : max(kTopPCandidates, a.N));
     if (K > 0) {
         float bound = kNegInf;
-        if (K < cn) bound = chunk_bound<E>(x, K, tab, ms);
+        if (K < cn) bound = chunk_bound<E>(x, K, cn, tab, ms);
         else __syncthreads();
         // candidates: elements >= thr; a finite threshold also excludes -inf scores
         float thr = -__FLT_MAX__;
