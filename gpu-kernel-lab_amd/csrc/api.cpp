@@ -55,18 +55,15 @@ int check_sizes(int32_t batch, int32_t vocab, int32_t dtype, int32_t max_top_k, 
 namespace kls {
 
 bool make_plan(int32_t batch, int32_t vocab, int32_t dtype, int32_t max_top_k, int32_t num_logprobs, Plan *p) {
-    // Elements per thread: the largest that still gives >= 2048 workgroups (8 per CU
-    // on 256 CUs); small batches use the smallest chunks to spread a row over CUs.
+    // Elements per thread: 32, the largest built variant.  Larger chunks amortise each
+    // workgroup's fixed work (history table, candidate bound) in the streaming pass and
+    // leave fewer chunk summaries and candidates for the row combine, which matters most
+    // for small batches.
     static const int kF32[] = {32, 16, 8, 4};
     static const int kBF16[] = {32, 16, 8};
     const int *cands = dtype == KLSAMPLE_FLOAT32 ? kF32 : kBF16;
     const int ncands = dtype == KLSAMPLE_FLOAT32 ? 4 : 3;
-    int e = cands[ncands - 1];
-    for (int i = 0; i < ncands; ++i) {
-        const int64_t chunk = (int64_t)kThreads * cands[i];
-        const int64_t s = (vocab + chunk - 1) / chunk;
-        if ((int64_t)batch * s >= 2048) { e = cands[i]; break; }
-    }
+    int e = cands[0];
     // KLSAMPLE_ELEMS_PER_THREAD pins E (tuning); ignored unless it names a built variant
     if (const char *env = getenv("KLSAMPLE_ELEMS_PER_THREAD")) {
         const int want = atoi(env);

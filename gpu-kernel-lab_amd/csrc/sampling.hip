@@ -262,10 +262,13 @@ __device__ __forceinline__ int wave_append(int *counter) {
 // ---------------------------------------------------------------------------------
 // Logits loaders: 16-byte vectors of fp32 (4) or bf16 (8) elements.
 template <typename TIn> struct Loader;
+// The streaming pass reads every logit once: its 16-byte loads are non-temporal.
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 template <> struct Loader<float> {
     static constexpr int VW = 4;
     __device__ static __forceinline__ void vec(const float *p, float *o) {
-        const float4 v = *reinterpret_cast<const float4 *>(p);
+        const f32x4 v = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(p));
         o[0] = v.x; o[1] = v.y; o[2] = v.z; o[3] = v.w;
     }
     __device__ static __forceinline__ float one(const float *p) { return *p; }
@@ -274,7 +277,7 @@ template <> struct Loader<uint16_t> {
     static constexpr int VW = 8;
     __device__ static __forceinline__ float bf(uint32_t h) { return __uint_as_float(h << 16); }
     __device__ static __forceinline__ void vec(const uint16_t *p, float *o) {
-        const uint4 v = *reinterpret_cast<const uint4 *>(p);
+        const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p));
         o[0] = bf(v.x & 0xffffu); o[1] = bf(v.x >> 16);
         o[2] = bf(v.y & 0xffffu); o[3] = bf(v.y >> 16);
         o[4] = bf(v.z & 0xffffu); o[5] = bf(v.z >> 16);
@@ -458,17 +461,14 @@ __device__ __forceinline__ float chunk_bound(const float (&x)[E], int K, int cn,
 // The row's candidates in their per-chunk slots: chunk c holds cnt[c] entries (cnt in
 // LDS).  Waves take chunks round robin, four at a time, and lanes take a chunk's
 // entries, so the loads of four chunks are in flight together.
-// Top-k rows store their candidates before the division by T (`temp` > 0 divides).
 struct CandSource {
     const Cand *cands;
     const int *cnt;
     int S, cap;
     float lo;
-    float temp;
     template <class F>
     __device__ __forceinline__ void visit(uint2 e, F &f) const {
-        float y = __uint_as_float(e.x);
-        if (temp > 0.f) y = __fdiv_rn(y, temp);
+        const float y = __uint_as_float(e.x);
         if (y >= lo) f(fkey(y), (int)e.y, y);
     }
     template <class F>
@@ -746,13 +746,27 @@ __device__ __forceinline__ int desc_key_idx(unsigned long long k) { return (int)
 // Sort n <= kThreads distinct keys ascending in place: each thread ranks one key
 // against all n (LDS broadcast reads) and stores it at its rank.  Two barriers,
 // against ~log2(n)^2/2 for a bitonic network.
+__device__ __forceinline__ int rank_of(const unsigned long long *sb, int n, unsigned long long mine) {
+    // broadcast reads of two keys at a time; they do not depend on each other, so the
+    // loads pipeline (sb is 16-byte aligned; an odd n reads one key past the end, which
+    // is not counted)
+    int rank = 0;
+#pragma unroll 4
+    for (int j = 0; j < n; j += 2) {
+        const ulonglong2 q = *reinterpret_cast<const ulonglong2 *>(&sb[j]);
+        rank += (q.x < mine) ? 1 : 0;
+        rank += (j + 1 < n && q.y < mine) ? 1 : 0;
+    }
+    return rank;
+}
+
 __device__ __forceinline__ void rank_sort(unsigned long long *sb, int n) {
     const int t = threadIdx.x;
     unsigned long long mine = 0ull;
     int rank = 0;
     if (t < n) {
         mine = sb[t];
-        for (int j = 0; j < n; ++j) rank += (sb[j] < mine) ? 1 : 0;
+        rank = rank_of(sb, n, mine);
     }
     __syncthreads();
     if (t < n) sb[rank] = mine;
@@ -1094,31 +1108,17 @@ __device__ __forceinline__ int topp_prefix(const unsigned long long *D, int n, d
 // ---------------------------------------------------------------------------------
 // One-wave finish of a row whose kept set is small: no barriers, one key per lane.
 
-// Bitonic sort of one 64-bit key per lane, ascending across the wave (~0 sorts last).
-__device__ __forceinline__ unsigned long long wave_sort(unsigned long long k) {
-    const int l = lane_id();
-#pragma unroll
-    for (int size = 2; size <= 64; size <<= 1) {
-#pragma unroll
-        for (int stride = size >> 1; stride > 0; stride >>= 1) {
-            const uint32_t olo = (uint32_t)__shfl_xor((int)(uint32_t)k, stride);
-            const uint32_t ohi = (uint32_t)__shfl_xor((int)(uint32_t)(k >> 32), stride);
-            const unsigned long long o = ((unsigned long long)ohi << 32) | olo;
-            const bool keep_min = ((l & stride) == 0) == ((l & size) == 0);
-            k = keep_min ? (o < k ? o : k) : (o > k ? o : k);
-        }
-    }
-    return k;
-}
-
-// Sort D[0..n) ascending (best first) in LDS: one wave for n <= 64, else the block.
+// Sort D[0..n) ascending (best first) in LDS: one wave ranks n <= 64 keys (the LDS
+// operations of one wave complete in order, so its reads precede its writes), else the
+// block.
 __device__ __forceinline__ void sort_top(unsigned long long *D, int n) {
     if (n <= 64) {
         if (wave_id() == 0) {
             const int l = lane_id();
-            unsigned long long k = l < n ? D[l] : ~0ull;
-            k = wave_sort(k);
-            if (l < n) D[l] = k;
+            const unsigned long long mine = l < n ? D[l] : ~0ull;
+            const int rank = rank_of(D, n, mine);
+            __builtin_amdgcn_wave_barrier();
+            if (l < n) D[rank] = mine;
         }
         __syncthreads();
     } else {
@@ -1131,7 +1131,7 @@ __device__ __forceinline__ void sort_top(unsigned long long *D, int n) {
 // entry of D crosses.  Wave-uniform; call from one whole wave.
 __device__ __forceinline__ int wave_topp(const unsigned long long *D, int n, double mref, double zref, float top_p) {
     const int l = lane_id();
-    const double w = l < n ? exp((double)desc_key_y(D[l]) - mref) : 0.0;
+    const double w = l < n ? (double)__expf(desc_key_y(D[l]) - (float)mref) : 0.0;
     const double excl = wave_shift_excl(wave_incl_scan(w));
     const unsigned long long cross = __ballot(l < n && excl > (double)top_p * zref);
     return cross ? __ffsll((long long)cross) - 1 : -1;
@@ -1195,14 +1195,25 @@ __device__ __forceinline__ void wave_write(const Args &a, int row, int mode, con
 }
 
 // Finish a sampled row in one wave: D[0..n) sorted best first, the first L kept
-// (1 <= L <= 64, L <= n), N <= 64.  Same results as finish_sampled.
+// (1 <= L <= 64, L <= n), N <= 64; `scr` is 128 free LDS words of 8 bytes.  Same
+// results as finish_sampled.  The draw ranks the kept entries by vocab index (broadcast
+// LDS reads), places their weights in index order and takes one prefix scan.
 __device__ __forceinline__ void wave_finish(const Args &a, int row, int mode, const klsample_row_params &p,
-                                            const unsigned long long *D, int n, int L, double mref) {
+                                            const unsigned long long *D, int n, int L, double mref,
+                                            unsigned long long *scr) {
     const int l = lane_id();
     const bool kept = l < L;
-    const float y = kept ? desc_key_y(D[l]) : kNegInf;
-    const int idx = kept ? desc_key_idx(D[l]) : 0x7fffffff;
-    const double w = kept ? exp((double)y - mref) : 0.0;
+    const unsigned long long key = kept ? D[l] : ~0ull;
+    const float y = kept ? desc_key_y(key) : kNegInf;
+    const int idx = kept ? desc_key_idx(key) : 0x7fffffff;
+    const double w = kept ? (double)__expf(y - (float)mref) : 0.0;
+    int rank = 0;
+#pragma unroll 4
+    for (int j = 0; j < L; j += 2) {
+        const ulonglong2 q = *reinterpret_cast<const ulonglong2 *>(&D[j]);
+        rank += (desc_key_idx(q.x) < idx) ? 1 : 0;
+        rank += (j + 1 < L && desc_key_idx(q.y) < idx) ? 1 : 0;
+    }
     const double zf = wave_reduce(w, OpSumD(), 0.0);
     RowOut r;
     r.path = 0;
@@ -1211,21 +1222,54 @@ __device__ __forceinline__ void wave_finish(const Args &a, int row, int mode, co
     r.cut_idx = (L < n && desc_key_y(D[L]) == r.cut) ? __builtin_amdgcn_readlane(idx, L - 1) : a.V;
     r.kept = L;
     r.log_norm = log(zf);
-    // inverse CDF in vocab order: kept mass at indices <= this lane's index
-    double c = 0.0;
-    for (int j = 0; j < L; ++j) {
-        const int ij = __builtin_amdgcn_readlane(idx, j);
-        const double wj = readlane(w, j);
-        c += (ij <= idx) ? wj : 0.0;
+    __builtin_amdgcn_wave_barrier();
+    if (kept) {
+        scr[rank] = __double_as_longlong(w);
+        scr[64 + rank] = (unsigned long long)(uint32_t)idx;
     }
+    __builtin_amdgcn_wave_barrier();
+    // lane i now holds the i-th smallest kept index: inverse CDF in vocab order
+    const double wi = kept ? __longlong_as_double(scr[l]) : 0.0;
+    const int ii = kept ? (int)(uint32_t)scr[64 + l] : 0;
+    const double cum = wave_incl_scan(wi);
     const double target = (double)p.uniform * zf;
-    int tok = wave_reduce((kept && c > target) ? idx : 0x7fffffff, OpMinI(), 0x7fffffff);
-    if (tok == 0x7fffffff) tok = wave_reduce((kept && w > 0.0) ? idx : -1, OpMaxI(), -1);
-    const unsigned long long at = __ballot(kept && idx == tok);
-    const int lt = at ? __ffsll((long long)at) - 1 : 0;
-    r.token = __builtin_amdgcn_readlane(idx, lt);
-    r.logprob = (double)readlane(y, lt) - mref - r.log_norm;
+    const unsigned long long over = __ballot(kept && cum > target);
+    int lt;
+    if (over) {
+        lt = __ffsll((long long)over) - 1;
+    } else {
+        const unsigned long long pos = __ballot(kept && wi > 0.0);
+        lt = pos ? 63 - __clzll((long long)pos) : 0;
+    }
+    r.token = __builtin_amdgcn_readlane(ii, lt);
+    const unsigned long long at = __ballot(kept && idx == r.token);
+    const int lo = at ? __ffsll((long long)at) - 1 : 0;
+    r.logprob = (double)readlane(y, lo) - mref - r.log_norm;
     wave_write(a, row, mode, r, D, min(a.N, L));
+}
+
+// Copy the entries of A[0..n) scoring >= t into D (capacity cap); returns their count
+// (D holds min(count, cap) of them).  Entries are counted first and one LDS atomic per
+// wave reserves their places.
+__device__ __forceinline__ int gather_ge(const unsigned long long *A, int n, float t, unsigned long long *D, int cap,
+                                         Misc &ms) {
+    if (threadIdx.x == 0) ms.ncand = 0;
+    __syncthreads();
+    int mine = 0;
+    for (int i = threadIdx.x; i < n; i += kThreads) mine += (desc_key_y(A[i]) >= t) ? 1 : 0;
+    const int incl = wave_incl_scan(mine);
+    int base = 0;
+    if (lane_id() == 63 && incl > 0) base = atomicAdd(&ms.ncand, incl);
+    base = readlane(base, 63) + incl - mine;
+    for (int i = threadIdx.x; i < n; i += kThreads) {
+        const unsigned long long k = A[i];
+        if (desc_key_y(k) >= t) {
+            if (base < cap) D[base] = k;
+            ++base;
+        }
+    }
+    __syncthreads();
+    return ms.ncand;
 }
 
 // ---------------------------------------------------------------------------------
@@ -1251,11 +1295,17 @@ __device__ __forceinline__ int select_top(const unsigned long long *A, int n, in
         __syncthreads();
         if (threadIdx.x == 0) ms.ncand = 0;
         __syncthreads();
+        int mine = 0;
+        for (int i = threadIdx.x; i < n; i += kThreads) mine += (bin(A[i]) >= b) ? 1 : 0;
+        const int incl = wave_incl_scan(mine);
+        int base = 0;
+        if (lane_id() == 63 && incl > 0) base = atomicAdd(&ms.ncand, incl);
+        base = readlane(base, 63) + incl - mine;
         for (int i = threadIdx.x; i < n; i += kThreads) {
             const unsigned long long k = A[i];
             if (bin(k) >= b) {
-                const int pos = wave_append(&ms.ncand);
-                if (pos < cap) D[pos] = k;
+                if (base < cap) D[base] = k;
+                ++base;
             }
         }
         __syncthreads();
@@ -1290,6 +1340,25 @@ __device__ __forceinline__ void emit_row(const Args &a, int row, int mode, const
     }
     __syncthreads();
     write_row(a, row, mode, r, count, ms);
+}
+
+// Smallest float x with fl(x / T) >= y (T > 0): fl(x / T) is non-decreasing in x, so
+// {x : fl(x / T) >= y} = {x : x >= that value}.  Found by stepping from fl(y * T), whose
+// distance from it is a few ulps; +inf when no finite x qualifies, -inf for y = -inf.
+__device__ __forceinline__ float quotient_threshold(float y, float T) {
+    if (!(y > kNegInf)) return kNegInf;
+    float x = __fmul_rn(y, T);
+    if (!(fabsf(x) <= __FLT_MAX__)) x = x > 0.f ? __FLT_MAX__ : -__FLT_MAX__;
+    for (int i = 0; i < 64 && !(__fdiv_rn(x, T) >= y); ++i) {
+        if (x == __FLT_MAX__) return __builtin_huge_valf();
+        x = nextafterf(x, __builtin_huge_valf());
+    }
+    for (int i = 0; i < 64; ++i) {
+        const float xp = nextafterf(x, kNegInf);
+        if (!(__fdiv_rn(xp, T) >= y)) break;
+        x = xp;
+    }
+    return x;
 }
 
 constexpr int kSpecLoads = 8;    // candidate pairs each thread requests with the chunk summaries
@@ -1373,9 +1442,13 @@ __device__ __forceinline__ bool combine_row(const Args &a, int row, const klsamp
     }
 
     // 3. F = { candidates >= lo } into A; every element of the row scoring >= lo is in
-    //    it.  Its key range [ia, ib] is tracked for the selection.
+    //    it.  Its key range is tracked for the selection.  Top-k rows keep their
+    //    candidates' scores before the division by T (the order is the same): they are
+    //    compared with xs, the smallest such score whose quotient reaches lo, and only
+    //    the final top set is divided.
     unsigned long long *A = reinterpret_cast<unsigned long long *>(raw);
     unsigned long long *D = A + kSortCap;
+    const float xs = (mode == kTopK) ? quotient_threshold(lo, p.temperature) : lo;
     uint32_t kmin = 0xffffffffu, kmax = 0u;
     auto take = [&](float y, int idx) {
         const int pos = wave_append(&ms.ncand);
@@ -1384,16 +1457,39 @@ __device__ __forceinline__ bool combine_row(const Args &a, int row, const klsamp
         kmin = min(kmin, k);
         kmax = max(kmax, k);
     };
+    {
+        // the requested slots: accepted ones counted first, one LDS atomic per wave
+        // reserves their places, then they are written
+        uint32_t acc = 0u;
 #pragma unroll
-    for (int i = 0; i < kSpecLoads; ++i) {
-        const int q = tid + i * kThreads;
-        const int c = q >> pshift;
-        if (c < nspec) {
-            const int nc = cnt[c], j = 2 * (q & (ppc - 1));
-            float y0 = __uint_as_float(spec[i].x), y1 = __uint_as_float(spec[i].z);
-            if (mode == kTopK) { y0 = __fdiv_rn(y0, p.temperature); y1 = __fdiv_rn(y1, p.temperature); }
-            if (j < nc && y0 >= lo) take(y0, (int)spec[i].y);
-            if (j + 1 < nc && y1 >= lo) take(y1, (int)spec[i].w);
+        for (int i = 0; i < kSpecLoads; ++i) {
+            const int q = tid + i * kThreads;
+            const int c = q >> pshift;
+            if (c < nspec) {
+                const int nc = cnt[c], j = 2 * (q & (ppc - 1));
+                if (j < nc && __uint_as_float(spec[i].x) >= xs) acc |= 1u << (2 * i);
+                if (j + 1 < nc && __uint_as_float(spec[i].z) >= xs) acc |= 2u << (2 * i);
+            }
+        }
+        const int mine = __popc(acc);
+        const int incl = wave_incl_scan(mine);
+        int base = 0;
+        if (lane_id() == 63 && incl > 0) base = atomicAdd(&ms.ncand, incl);
+        base = readlane(base, 63) + incl - mine;
+#pragma unroll
+        for (int i = 0; i < kSpecLoads; ++i) {
+            if (acc & (1u << (2 * i))) {
+                if (base < kSortCap) A[base] = desc_key(__uint_as_float(spec[i].x), (int)spec[i].y);
+                ++base;
+                const uint32_t k = fkey(__uint_as_float(spec[i].x));
+                kmin = min(kmin, k); kmax = max(kmax, k);
+            }
+            if (acc & (2u << (2 * i))) {
+                if (base < kSortCap) A[base] = desc_key(__uint_as_float(spec[i].z), (int)spec[i].w);
+                ++base;
+                const uint32_t k = fkey(__uint_as_float(spec[i].z));
+                kmin = min(kmin, k); kmax = max(kmax, k);
+            }
         }
     }
     if (want_cands) {
@@ -1402,8 +1498,7 @@ __device__ __forceinline__ bool combine_row(const Args &a, int row, const klsamp
             const int nc = cnt[c];
             for (int j = (c < nspec ? 2 * ppc : 0) + lane_id(); j < nc; j += 64) {
                 const Cand cd = rc[(size_t)c * a.cand_cap + j];
-                const float y = (mode == kTopK) ? __fdiv_rn(cd.y, p.temperature) : cd.y;
-                if (y >= lo) take(y, cd.idx);
+                if (cd.y >= xs) take(cd.y, cd.idx);
             }
         }
     }
@@ -1429,7 +1524,7 @@ __device__ __forceinline__ bool combine_row(const Args &a, int row, const klsamp
         // the candidate slots
         const int R = (mode == kTopK) ? p.top_k : (mode == kTopP ? kThreads : N);
         if (R < 1 || R > kSortCap) return false;
-        const CandSource src{rc, cnt, S, a.cand_cap, lo, mode == kTopK ? p.temperature : 0.f};
+        const CandSource src{rc, cnt, S, a.cand_cap, xs};
         ylo = fkey_inv(select_kth(src, (uint32_t)R, ms));
         nF = gather_keys(src, ylo, A, kSortCap, ms);
         if (nF > kSortCap) return false;
@@ -1508,20 +1603,35 @@ __device__ __forceinline__ bool combine_row(const Args &a, int row, const klsamp
     }
 
     if (mode == kTopK) {
-        // top-k: the kk best and every tie of the kk-th, then top-p on them
-        const int lk = best(p.top_k);
-        if (lk < 0) return false;
+        // top-k: the kk best and every tie of the kk-th, then top-p on them.  The kk-th
+        // largest score before division gives the kk-th quotient; the top set is every
+        // candidate whose quotient reaches it (ties created by the division included),
+        // divided and sorted in final space.
+        const int kk = p.top_k;
+        float xt = kNegInf;
+        if (nF > kk) {
+            if (best(kk) < 0) return false;
+            xt = quotient_threshold(__fdiv_rn(desc_key_y(D[kk - 1]), p.temperature), p.temperature);
+        }
+        const int lk = gather_ge(A, nF, xt, D, kSortCap, ms);
+        if (lk > kSortCap) return false;
+        for (int i = tid; i < lk; i += kThreads) {
+            const unsigned long long k = D[i];
+            D[i] = desc_key(__fdiv_rn(desc_key_y(k), p.temperature), desc_key_idx(k));
+        }
+        __syncthreads();
+        sort_top(D, lk);
         const double mref = (double)desc_key_y(D[0]);
         const bool topp = (p.flags & KLSAMPLE_ROW_TOP_P) != 0;
         if (lk <= 64 && N <= 64) {
             if (wave_id() == 0) {
                 int L = lk;
                 if (topp) {
-                    const double w = lane_id() < lk ? exp((double)desc_key_y(D[lane_id()]) - mref) : 0.0;
+                    const double w = lane_id() < lk ? (double)__expf(desc_key_y(D[lane_id()]) - (float)mref) : 0.0;
                     const int cut = wave_topp(D, lk, mref, wave_reduce(w, OpSumD(), 0.0), p.top_p);
                     if (cut > 0) L = cut;
                 }
-                wave_finish(a, row, mode, p, D, lk, L, mref);
+                wave_finish(a, row, mode, p, D, lk, L, mref, A);
             }
             return true;
         }
@@ -1561,7 +1671,7 @@ __device__ __forceinline__ bool combine_row(const Args &a, int row, const klsamp
         L = n;                            // the candidates are the whole row
     }
     if (L <= 64 && N <= 64) {
-        if (wave_id() == 0) wave_finish(a, row, mode, p, D, n, L, mref);
+        if (wave_id() == 0) wave_finish(a, row, mode, p, D, n, L, mref, A);
         return true;
     }
     finish_sampled(a, row, mode, p, D, n, L, mref, ms);
@@ -1609,7 +1719,7 @@ struct ScanLds {
 // needs no per-element branch; the listed elements join the sums and the candidates
 // separately.  The bound over the remaining elements stays a valid lower bound.
 template <typename TIn, int E>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(E >= 32 ? 4 : (E >= 16 && sizeof(TIn) == 2) ? 7 : 8))) void scan_kernel(Args a) {
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(E >= 32 ? 4 : E >= 16 ? 7 : 8))) void scan_kernel(Args a) {
     constexpr int VW = Loader<TIn>::VW;
     constexpr int NV = E / VW;
     constexpr int C = kThreads * E;

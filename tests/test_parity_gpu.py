@@ -223,3 +223,16 @@ def test_large_top_k_and_top_n():
     rows = sample_rows(x, None, params, u)
     out = run(x, params, None, u)
     check(out, rows, params)
+
+
+@pytest.mark.parametrize('elems', ['4', '8', '16'])
+def test_other_chunk_sizes(elems, monkeypatch):
+    """The smaller chunk variants (selected by KLSAMPLE_ELEMS_PER_THREAD, read per call)
+    give the same results as the default."""
+    say(f'chunk variant E={elems}')
+    monkeypatch.setenv('KLSAMPLE_ELEMS_PER_THREAD', elems)
+    for name, batch in (('mixed_b64', 16), ('throughput_b256_v151936', 8), ('latency_b1', None)):
+        w = _with_logprobs(workloads.make(name, batch=batch), 4)
+        rows = sample_rows(w.logits, w.histories, w.params, w.uniforms)
+        out = run(w.logits, w.params, w.histories, w.uniforms, probs=True)
+        check(out, rows, w.params, probs=True)
