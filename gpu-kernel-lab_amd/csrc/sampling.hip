@@ -105,7 +105,6 @@ struct ScanMisc : Red {
     uint32_t wbound[kWaves];
     uint32_t bound_key;
     int ncand;
-    int nhits;
 };
 
 struct Misc : Red {
@@ -1326,22 +1325,6 @@ __device__ __forceinline__ int select_top(const unsigned long long *A, int n, in
     return R + block_sum(c, ms);
 }
 
-// Emit a row's outputs with its top-N list in D[0..count): one wave when the list is
-// short, else the block writer.
-__device__ __forceinline__ void emit_row(const Args &a, int row, int mode, const RowOut &r,
-                                         const unsigned long long *D, int count, Misc &ms) {
-    if (count <= 64 && a.N <= 64) {
-        if (wave_id() == 0) wave_write(a, row, mode, r, D, count);
-        return;
-    }
-    for (int t = threadIdx.x; t < count; t += kThreads) {
-        ms.topn_idx[t] = desc_key_idx(D[t]);
-        ms.topn_y[t] = desc_key_y(D[t]);
-    }
-    __syncthreads();
-    write_row(a, row, mode, r, count, ms);
-}
-
 // Smallest float x with fl(x / T) >= y (T > 0): fl(x / T) is non-decreasing in x, so
 // {x : fl(x / T) >= y} = {x : x >= that value}.  Found by stepping from fl(y * T), whose
 // distance from it is a few ulps; +inf when no finite x qualifies, -inf for y = -inf.
@@ -1359,6 +1342,128 @@ __device__ __forceinline__ float quotient_threshold(float y, float T) {
         x = xp;
     }
     return x;
+}
+
+// Block: the entries of A[0..n) (n > R >= 1) in the linear histogram bins (256 over
+// [ylo, yhi]) at or above the bin of the R-th largest, into D (capacity cap), unsorted.
+// ms.hist must be zero and ms.ib the zero counter.  Returns their count (D holds at
+// most cap of them), or -1 for a degenerate range.  Two barriers: every wave finds the
+// bin from the same histogram.
+__device__ __forceinline__ int hist_gather(const unsigned long long *A, int n, int R, float ylo, float yhi,
+                                           unsigned long long *D, int cap, Misc &ms) {
+    const float span = yhi - ylo;
+    const float scale = 256.f / span;
+    if (!(span > 0.f) || !(scale <= __FLT_MAX__)) return -1;
+    auto bin = [&](unsigned long long k) { return min(255, (int)((desc_key_y(k) - ylo) * scale)); };
+    for (int i = threadIdx.x; i < n; i += kThreads) atomicAdd(&ms.hist[bin(A[i])], 1u);
+    __syncthreads();
+    const int l = lane_id();
+    uint32_t c[4], sum = 0u;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) { c[j] = ms.hist[255 - 4 * l - j]; sum += c[j]; }
+    const uint32_t incl = wave_incl_scan(sum);
+    const unsigned long long reach = __ballot(incl >= (uint32_t)R);
+    const int fl = reach ? __ffsll((long long)reach) - 1 : 63;
+    int b = 0;
+    if (l == fl) {
+        uint32_t acc = incl - sum;
+        b = 252 - 4 * l;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            if (acc + c[j] >= (uint32_t)R) { b = 255 - 4 * l - j; break; }
+            acc += c[j];
+        }
+    }
+    b = __builtin_amdgcn_readlane(b, fl);
+    int mine = 0;
+    for (int i = threadIdx.x; i < n; i += kThreads) mine += (bin(A[i]) >= b) ? 1 : 0;
+    const int pincl = wave_incl_scan(mine);
+    int base = 0;
+    if (l == 63 && pincl > 0) base = atomicAdd(&ms.ib, pincl);
+    base = readlane(base, 63) + pincl - mine;
+    for (int i = threadIdx.x; i < n; i += kThreads) {
+        const unsigned long long k = A[i];
+        if (bin(k) >= b) {
+            if (base < cap) D[base] = k;
+            ++base;
+        }
+    }
+    __syncthreads();
+    return ms.ib;
+}
+
+// One wave: sort D[0..t) (t <= 256, distinct keys) ascending, up to four keys per lane.
+__device__ __forceinline__ void wave_rank_sort(unsigned long long *D, int t) {
+    const int l = lane_id();
+    unsigned long long key[4];
+    int rk[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int i = l + 64 * j;
+        key[j] = i < t ? D[i] : ~0ull;
+        rk[j] = i < t ? rank_of(D, t, key[j]) : 0;
+    }
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+        if (l + 64 * j < t) D[rk[j]] = key[j];
+    __builtin_amdgcn_wave_barrier();
+}
+
+// One wave finishes a top-k row.  D[0..t) (t <= 256) holds the candidates of the
+// histogram bins at or above the kk-th one's, as scores before the division by T; A[0..nF)
+// holds every candidate.  Sorts D, takes the kk-th score's quotient, gathers every
+// candidate whose quotient reaches it (ties created by the division included), divides
+// and sorts them, applies top-p and writes the row.  Returns false, having written
+// nothing, when that top set exceeds 64 entries.
+__device__ __forceinline__ bool topk_wave_tail(const Args &a, int row, int mode, const klsample_row_params &p,
+                                               unsigned long long *A, int nF, unsigned long long *D, int t, int kk) {
+    const int l = lane_id();
+    wave_rank_sort(D, t);
+    const float xt = quotient_threshold(__fdiv_rn(desc_key_y(D[kk - 1]), p.temperature), p.temperature);
+    unsigned long long *E = D + 256;
+    int mine = 0;
+    for (int i = l; i < nF; i += 64) mine += (desc_key_y(A[i]) >= xt) ? 1 : 0;
+    const int incl = wave_incl_scan(mine);
+    const int lk = readlane(incl, 63);
+    if (lk > 64) return false;
+    int pos = incl - mine;
+    for (int i = l; i < nF; i += 64) {
+        const unsigned long long k = A[i];
+        const float x = desc_key_y(k);
+        if (x >= xt) E[pos++] = desc_key(__fdiv_rn(x, p.temperature), desc_key_idx(k));
+    }
+    __builtin_amdgcn_wave_barrier();
+    const unsigned long long mk = l < lk ? E[l] : ~0ull;
+    const int rank = rank_of(E, lk, mk);
+    __builtin_amdgcn_wave_barrier();
+    if (l < lk) E[rank] = mk;
+    __builtin_amdgcn_wave_barrier();
+    const double mref = (double)desc_key_y(E[0]);
+    int L = lk;
+    if (p.flags & KLSAMPLE_ROW_TOP_P) {
+        const double w = l < lk ? (double)__expf(desc_key_y(E[l]) - (float)mref) : 0.0;
+        const int cut = wave_topp(E, lk, mref, wave_reduce(w, OpSumD(), 0.0), p.top_p);
+        if (cut > 0) L = cut;
+    }
+    wave_finish(a, row, mode, p, E, lk, L, mref, A);
+    return true;
+}
+
+// Emit a row's outputs with its top-N list in D[0..count): one wave when the list is
+// short, else the block writer.
+__device__ __forceinline__ void emit_row(const Args &a, int row, int mode, const RowOut &r,
+                                         const unsigned long long *D, int count, Misc &ms) {
+    if (count <= 64 && a.N <= 64) {
+        if (wave_id() == 0) wave_write(a, row, mode, r, D, count);
+        return;
+    }
+    for (int t = threadIdx.x; t < count; t += kThreads) {
+        ms.topn_idx[t] = desc_key_idx(D[t]);
+        ms.topn_y[t] = desc_key_y(D[t]);
+    }
+    __syncthreads();
+    write_row(a, row, mode, r, count, ms);
 }
 
 constexpr int kSpecLoads = 8;    // candidate pairs each thread requests with the chunk summaries
@@ -1395,12 +1500,15 @@ __device__ __forceinline__ bool combine_row(const Args &a, int row, const klsamp
     const bool has = tid < S;
     const ChunkStat s0 = load_stat(st + min(tid, S - 1));
 
-    // 2. Row max, candidate bound, finite count, overflow; then sum-exp and argmax.
+    // 2. Row max, candidate bound, finite count, overflow (bit 0) and whether any chunk
+    //    has candidates past the requested slots (bit 1); then sum-exp and argmax.
     float m = kNegInf, lo = kNegInf;
     int nfinite = 0, ovf = 0;
     if (has) {
         m = s0.m; lo = s0.y_thr; nfinite = s0.nfinite; ovf = s0.overflow;
-        cnt[tid] = min(s0.ncand, a.cand_cap);
+        const int nc = min(s0.ncand, a.cand_cap);
+        cnt[tid] = nc;
+        if (tid >= nspec ? nc > 0 : nc > 2 * ppc) ovf |= 2;
     }
     for (int c = tid + kThreads; c < S; c += kThreads) {
         const ChunkStat s = st[c];
@@ -1408,8 +1516,11 @@ __device__ __forceinline__ bool combine_row(const Args &a, int row, const klsamp
         lo = fmaxf(lo, s.y_thr);
         nfinite += s.nfinite;
         ovf |= s.overflow;
-        cnt[c] = min(s.ncand, a.cand_cap);
+        const int nc = min(s.ncand, a.cand_cap);
+        cnt[c] = nc;
+        if (c >= nspec ? nc > 0 : nc > 2 * ppc) ovf |= 2;
     }
+    ms.hist[tid] = 0u;   // kThreads == 256 bins, used by the selection below
     m = wave_reduce(m, OpMaxF(), kNegInf);
     lo = wave_reduce(lo, OpMaxF(), kNegInf);
     nfinite = wave_reduce(nfinite, OpSumI(), 0);
@@ -1418,7 +1529,7 @@ __device__ __forceinline__ bool combine_row(const Args &a, int row, const klsamp
         ms.rf[0][wave_id()] = m; ms.rf[1][wave_id()] = lo;
         ms.ri[0][wave_id()] = nfinite; ms.ri[1][wave_id()] = ovf;
     }
-    if (tid == 0) { ms.ncand = 0; ms.ia = 0x7fffffff; ms.kmin = 0xffffffffu; ms.kmax = 0u; }
+    if (tid == 0) { ms.ncand = 0; ms.ia = 0x7fffffff; ms.ib = 0; ms.kmin = 0xffffffffu; ms.kmax = 0u; }
     __syncthreads();
     m = ms.rf[0][0]; lo = ms.rf[1][0]; nfinite = ms.ri[0][0]; ovf = ms.ri[1][0];
 #pragma unroll
@@ -1426,7 +1537,8 @@ __device__ __forceinline__ bool combine_row(const Args &a, int row, const klsamp
         m = fmaxf(m, ms.rf[0][w]); lo = fmaxf(lo, ms.rf[1][w]);
         nfinite += ms.ri[0][w]; ovf |= ms.ri[1][w];
     }
-    if (ovf) return false;   // a chunk's candidates overflowed (massive ties)
+    if (ovf & 1) return false;   // a chunk's candidates overflowed (massive ties)
+    const bool need_rest = (ovf & 2) != 0;
     int arg = 0x7fffffff;
     double Z = 0.0;
     if (mode != kTopK) {
@@ -1465,11 +1577,10 @@ __device__ __forceinline__ bool combine_row(const Args &a, int row, const klsamp
         for (int i = 0; i < kSpecLoads; ++i) {
             const int q = tid + i * kThreads;
             const int c = q >> pshift;
-            if (c < nspec) {
-                const int nc = cnt[c], j = 2 * (q & (ppc - 1));
-                if (j < nc && __uint_as_float(spec[i].x) >= xs) acc |= 1u << (2 * i);
-                if (j + 1 < nc && __uint_as_float(spec[i].z) >= xs) acc |= 2u << (2 * i);
-            }
+            const int nc0 = cnt[min(c, kMaxChunksLds - 1)];   // read unconditionally
+            const int nc = (c < nspec) ? nc0 : 0, j = 2 * (q & (ppc - 1));
+            if (j < nc && __uint_as_float(spec[i].x) >= xs) acc |= 1u << (2 * i);
+            if (j + 1 < nc && __uint_as_float(spec[i].z) >= xs) acc |= 2u << (2 * i);
         }
         const int mine = __popc(acc);
         const int incl = wave_incl_scan(mine);
@@ -1492,7 +1603,7 @@ __device__ __forceinline__ bool combine_row(const Args &a, int row, const klsamp
             }
         }
     }
-    if (want_cands) {
+    if (need_rest) {
         // the rest: chunks beyond the requested ones, and slots past the requested pairs
         for (int c = wave_id(); c < S; c += kWaves) {
             const int nc = cnt[c];
@@ -1608,6 +1719,18 @@ __device__ __forceinline__ bool combine_row(const Args &a, int row, const klsamp
         // candidate whose quotient reaches it (ties created by the division included),
         // divided and sorted in final space.
         const int kk = p.top_k;
+        if (nF > kk && N <= 64) {
+            // one histogram pass isolates the kk best, then one wave does the rest
+            const int t = hist_gather(A, nF, kk, ylo, yhi, D, kSortCap, ms);
+            if (t >= 0 && t <= 256) {
+                if (wave_id() == 0) {
+                    const bool done = topk_wave_tail(a, row, mode, p, A, nF, D, t, kk);
+                    if (lane_id() == 0) ms.flag = done ? 1 : 0;
+                }
+                __syncthreads();
+                if (ms.flag) return true;
+            }
+        }
         float xt = kNegInf;
         if (nF > kk) {
             if (best(kk) < 0) return false;
@@ -1649,6 +1772,19 @@ __device__ __forceinline__ bool combine_row(const Args &a, int row, const klsamp
 
     // top-p alone: the best 64 (one wave), then the best 256, then every candidate
     const double mref = (double)m;
+    if (nF > 64 && N <= 64) {
+        const int t = hist_gather(A, nF, 64, ylo, yhi, D, kSortCap, ms);
+        if (t >= 0 && t <= 256) {
+            if (wave_id() == 0) {
+                wave_rank_sort(D, t);
+                const int cut = wave_topp(D, min(t, 64), mref, Z, p.top_p);
+                if (cut > 0) wave_finish(a, row, mode, p, D, t, cut, mref, A);
+                if (lane_id() == 0) ms.flag = cut > 0 ? 1 : 0;
+            }
+            __syncthreads();
+            if (ms.flag) return true;
+        }
+    }
     int n = 0, L = -1;
     for (int R = 64;; R = (R < kThreads) ? kThreads : nF) {
         if (R > nF) R = nF;
@@ -1693,16 +1829,18 @@ __device__ __forceinline__ void map_block(const Args &a, int &row, int &chunk) {
 }
 
 // LDS of the streaming pass.  Penalty phase: the chunk's history counts (16 bits, two
-// per word), the list of distinct history elements of the chunk and, per thread, a
-// mask of its register slots holding one.  Later, the fallback bound's group keys.
-constexpr int kHitCap = 2 * kThreads;   // distinct history elements per chunk on the list path
+// per word), per thread a mask of its register slots holding a history element, and
+// per wave a staging area where up to kStageLanes lanes at a time spill their
+// registers to penalise them.  Later, the fallback bound's group keys.
+constexpr int kStageLanes = 16;
 
 template <int E>
 struct ScanLds {
     static constexpr int C = kThreads * E;
     static constexpr int counts = C * 2;
-    static constexpr int hits_off = counts;
-    static constexpr int mask_off = hits_off + kHitCap * 2;
+    static constexpr int stride = E + 4;   // floats per staged lane (padded against bank conflicts)
+    static constexpr int stage_off = counts;
+    static constexpr int mask_off = stage_off + kWaves * kStageLanes * stride * 4;
     static constexpr int penalty = mask_off + kThreads * 4;
     static constexpr int keys = kThreads * (E < 16 ? E : 16) * 4;   // fallback bound (later)
     static constexpr int value = penalty > keys ? penalty : keys;
@@ -1712,18 +1850,17 @@ struct ScanLds {
 // lets eight workgroups share a CU; the register budget is capped so that five
 // (32 elements per thread) or eight waves per SIMD fit, to hide HBM latency.
 //
-// Penalties: the row's history ids are counted into an LDS table; the first thread
-// to count an element lists it, marks it in its owner's slot mask, and later applies
-// the penalty to it alone (one element per thread).  The owners replace listed
-// elements by -inf in their registers, so the dense work (bound, candidates, sums)
-// needs no per-element branch; the listed elements join the sums and the candidates
-// separately.  The bound over the remaining elements stays a valid lower bound.
+// Penalties: the row's history ids are counted into an LDS table and mark their
+// element in its owner's slot mask (atomics whose results nobody waits for).  A lane
+// owning marked elements spills its registers to its wave's LDS staging area,
+// penalises the marked ones there (one per set mask bit) and reloads them, so the
+// dense work that follows (bound, candidates, sums) sees final scores everywhere
+// with no per-element branch.
 template <typename TIn, int E>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(E >= 32 ? 4 : E >= 16 ? 7 : 8))) void scan_kernel(Args a) {
     constexpr int VW = Loader<TIn>::VW;
     constexpr int NV = E / VW;
     constexpr int C = kThreads * E;
-    constexpr int kHitsPer = kHitCap / kThreads;
     __shared__ __attribute__((aligned(16))) unsigned char raw[ScanLds<E>::value];
     __shared__ ScanMisc ms;
 
@@ -1737,7 +1874,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(E >= 3
     const int c0 = chunk * C;
     const int cn = min(C, V - c0);
     const TIn *src = reinterpret_cast<const TIn *>(a.logits) + (int64_t)row * a.row_stride + c0;
-    if (tid == 0) { ms.ncand = 0; ms.nhits = 0; }
+    if (tid == 0) ms.ncand = 0;
 
     // History of a penalised row.  Its first ids are requested before the logits, so
     // the count table is built while the logits are in flight.  Counts are 16-bit
@@ -1751,7 +1888,6 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(E >= 3
     const int H = h1 - h0;
     const bool packed = H > 0 && H < 65536;
     uint32_t *tab = reinterpret_cast<uint32_t *>(raw);
-    uint16_t *hits = reinterpret_cast<uint16_t *>(raw + ScanLds<E>::hits_off);
     uint32_t *hmask = reinterpret_cast<uint32_t *>(raw + ScanLds<E>::mask_off);
     int hid[8];
     if (packed) {
@@ -1780,28 +1916,16 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(E >= 3
         }
     }
 
-    // penalised scores of this thread's listed history elements (-inf: none)
-    float hy[kHitsPer];
-    int hix[kHitsPer];
-#pragma unroll
-    for (int j = 0; j < kHitsPer; ++j) { hy[j] = kNegInf; hix[j] = 0; }
-
     if (packed) {
         __syncthreads();   // table cleared
         // (the ids were loaded from clamped positions: h >= h1 marks a repeat, not an id)
         auto count = [&](int id, int h) {
-            const unsigned rel = (unsigned)(id - c0);
-            if (h < h1 && id >= 0 && rel < (unsigned)cn) {
-                const uint32_t sh = (rel & 1u) * 16u;
-                const uint32_t old = atomicAdd(&tab[rel >> 1], 1u << sh);
-                if (((old >> sh) & 0xffffu) == 0u) {
-                    // first count of this element: list it, mark its owner's slot
-                    const int pos = atomicAdd(&ms.nhits, 1);
-                    if (pos < kHitCap) hits[pos] = (uint16_t)rel;
-                    const unsigned owner = (rel / VW) % kThreads;
-                    const unsigned slot = (rel / (VW * kThreads)) * VW + rel % VW;
-                    atomicOr(&hmask[owner], 1u << slot);
-                }
+            const unsigned rel = (unsigned)id - (unsigned)c0;   // negative ids wrap past cn
+            if (h < h1 && rel < (unsigned)cn) {
+                const unsigned owner = (rel / VW) % kThreads;
+                const unsigned slot = (rel / (VW * kThreads)) * VW + rel % VW;
+                atomicAdd(&tab[rel >> 1], 1u << ((rel & 1u) * 16u));
+                atomicOr(&hmask[owner], 1u << slot);
             }
         };
 #pragma unroll
@@ -1813,46 +1937,36 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(E >= 3
             for (int j = 0; j < 8; ++j) count(hid[j], hb + j * kThreads);
         }
         __syncthreads();
-        const int nh = ms.nhits;
-        if (nh <= kHitCap) {
-            // listed elements: original logit re-read (cached), penalty, temperature
+        const uint32_t mk = hmask[tid];
+        // rounds of at most kStageLanes owner lanes per wave; the staging area is the
+        // wave's own, and a wave's LDS accesses complete in order
+        uint64_t pend = __ballot(mk != 0u);
+        float *stage = reinterpret_cast<float *>(raw + ScanLds<E>::stage_off) +
+                       wave_id() * (kStageLanes * ScanLds<E>::stride);
+        const uint64_t below = (1ull << lane_id()) - 1ull;
+        while (pend) {
+            const int rank = __popcll(pend & below);
+            const bool mine = ((pend >> lane_id()) & 1ull) && rank < kStageLanes;
+            if (mine) {
+                float *sl = stage + rank * ScanLds<E>::stride;
 #pragma unroll
-            for (int j = 0; j < kHitsPer; ++j) {
-                const int k = tid + j * kThreads;
-                if (k < nh) {
-                    const int rel = hits[k];
-                    const uint32_t c = (tab[rel >> 1] >> ((rel & 1) * 16)) & 0xffffu;
-                    float y = penalize(Loader<TIn>::one(src + rel), c, p);
-                    if (divided) y = __fdiv_rn(y, p.temperature);
-                    hy[j] = y;
-                    hix[j] = rel;
+                for (int v = 0; v < E / 4; ++v)
+                    *reinterpret_cast<float4 *>(sl + 4 * v) = make_float4(x[4 * v], x[4 * v + 1], x[4 * v + 2], x[4 * v + 3]);
+                uint32_t m = mk;
+                while (m) {
+                    const int e = __builtin_ctz(m);
+                    m &= m - 1u;
+                    const int rel = ((e / VW) * kThreads + tid) * VW + e % VW;
+                    sl[e] = penalize(sl[e], (tab[rel >> 1] >> ((rel & 1) * 16)) & 0xffffu, p);
+                }
+#pragma unroll
+                for (int v = 0; v < E / 4; ++v) {
+                    const float4 q = *reinterpret_cast<const float4 *>(sl + 4 * v);
+                    x[4 * v] = q.x; x[4 * v + 1] = q.y; x[4 * v + 2] = q.z; x[4 * v + 3] = q.w;
                 }
             }
-            // owners drop their listed elements from the dense work
-            const uint32_t mk = hmask[tid];
-#pragma unroll
-            for (int e = 0; e < E; ++e) x[e] = ((mk >> e) & 1u) ? kNegInf : x[e];
-        } else {
-            // more distinct history elements than the list holds: per-element penalties
-#pragma unroll
-            for (int v = 0; v < NV; ++v) {
-                const int li = (v * kThreads + tid) * VW;   // even: element pairs share words
-                uint32_t w[VW / 2];
-                if constexpr (VW == 4) {
-                    const uint2 q = *reinterpret_cast<const uint2 *>(&tab[li >> 1]);
-                    w[0] = q.x; w[1] = q.y;
-                } else {
-                    const uint4 q = *reinterpret_cast<const uint4 *>(&tab[li >> 1]);
-                    w[0] = q.x; w[1] = q.y; w[2] = q.z; w[3] = q.w;
-                }
-#pragma unroll
-                for (int e = 0; e < VW; ++e) {
-                    const uint32_t c = (w[e >> 1] >> ((e & 1) * 16)) & 0xffffu;
-                    if (c) x[v * VW + e] = penalize(x[v * VW + e], c, p);
-                }
-            }
+            pend &= ~__ballot(mine);
         }
-        __syncthreads();
     } else if (H > 0) {
         // 32-bit counts over slices of the chunk that fit the table
         constexpr int RC = ScanLds<E>::value / 4;
@@ -1897,8 +2011,6 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(E >= 3
         float mt = kNegInf;
 #pragma unroll
         for (int e = 0; e < E; ++e) mt = fmaxf(mt, x[e]);
-#pragma unroll
-        for (int j = 0; j < kHitsPer; ++j) mt = fmaxf(mt, hy[j]);
         const float m = block_max(mt, ms);
         if (mode == kGreedy) {
             int at = 0x7fffffff;
@@ -1909,9 +2021,6 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(E >= 3
                 for (int e = 0; e < VW; ++e)
                     if (x[v * VW + e] == m && li + e < cn && li + e < at) at = li + e;
             }
-#pragma unroll
-            for (int j = 0; j < kHitsPer; ++j)
-                if (hy[j] == m && hix[j] < at) at = hix[j];
             at = block_min(at, ms);
             st.arg = (at == 0x7fffffff) ? 0x7fffffff : c0 + at;
         }
@@ -1922,11 +2031,6 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(E >= 3
             for (int e = 0; e < E; ++e) {
                 z += (double)exp_fast(x[e] - m);
                 nfin += (x[e] > kNegInf) ? 1 : 0;
-            }
-#pragma unroll
-            for (int j = 0; j < kHitsPer; ++j) {
-                z += (double)exp_fast(hy[j] - m);
-                nfin += (hy[j] > kNegInf) ? 1 : 0;
             }
         }
         st.z = block_sumd(z, ms);
@@ -1955,8 +2059,6 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(E >= 3
         int my = 0;
 #pragma unroll
         for (int e = 0; e < E; ++e) my += (x[e] >= thr) ? 1 : 0;
-#pragma unroll
-        for (int j = 0; j < kHitsPer; ++j) my += (hy[j] >= thr) ? 1 : 0;
         const int incl = wave_incl_scan(my);
         const int wtot = readlane(incl, 63);
         int wbase = 0;
@@ -1982,18 +2084,6 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(E >= 3
                     }
                     ++pos;
                 }
-            }
-        }
-#pragma unroll
-        for (int j = 0; j < kHitsPer; ++j) {
-            if (hy[j] >= thr) {
-                if (pos < cap) {
-                    Cand cd;
-                    cd.y = hy[j];
-                    cd.idx = c0 + hix[j];
-                    out[pos] = cd;
-                }
-                ++pos;
             }
         }
         __syncthreads();
