@@ -32,6 +32,8 @@
 #include <math.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "internal.h"
 
 namespace kls {
@@ -385,15 +387,15 @@ __device__ __forceinline__ float block_group_bound(const float (&x)[E], int K, u
     if (wave_id() == 0) {
         const int lane = lane_id();
         uint32_t t = 0u;
-        // re-read the keys every step (volatile keeps the compiler from hoisting all
-        // of them into registers for the whole kernel)
-        const volatile uint32_t *vk = keys;
 #pragma unroll 1
         for (int bit = 31; bit >= 8; --bit) {
+            // re-read the keys every step: the empty asm keeps the compiler from
+            // hoisting all of them into registers for the whole kernel
+            __asm__ volatile("" ::: "memory");
             const uint32_t cand = t | (1u << bit);
             int c = 0;
 #pragma unroll 4
-            for (int j = 0; j < PER; ++j) c += __popcll(__ballot(vk[j * 64 + lane] >= cand));
+            for (int j = 0; j < PER; ++j) c += __popcll(__ballot(keys[j * 64 + lane] >= cand));
             if (c >= K) t = cand;
         }
         if (lane == 0) ms.bound_key = t;
@@ -1886,18 +1888,23 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(E >= 3
         h1 = a.hist_off[row + 1];
     }
     const int H = h1 - h0;
-    const bool packed = H > 0 && H < 65536;
+    // 16-bit counts (two per word) cover the chunk when no count can reach 65536;
+    // longer histories count in 32 bits over each half of the chunk in turn
+    const bool packed = H < 65536;
     uint32_t *tab = reinterpret_cast<uint32_t *>(raw);
     uint32_t *hmask = reinterpret_cast<uint32_t *>(raw + ScanLds<E>::mask_off);
-    int hid[8];
-    if (packed) {
-        // clamped addresses, unpredicated loads: all eight stay in flight together
-#pragma unroll
-        for (int j = 0; j < 8; ++j) hid[j] = a.hist_ids[min(h0 + tid + j * kThreads, h1 - 1)];
+    auto clear = [&]() {
         uint4 *t4 = reinterpret_cast<uint4 *>(raw);
 #pragma unroll
         for (int i = tid; i < C / 8; i += kThreads) t4[i] = make_uint4(0u, 0u, 0u, 0u);
         hmask[tid] = 0u;
+    };
+    int hid[8];
+    if (H > 0) {
+        // clamped addresses, unpredicated loads: all eight stay in flight together
+#pragma unroll
+        for (int j = 0; j < 8; ++j) hid[j] = a.hist_ids[min(h0 + tid + j * kThreads, h1 - 1)];
+        clear();
     }
 
     float x[E];
@@ -1916,82 +1923,85 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(E >= 3
         }
     }
 
-    if (packed) {
-        __syncthreads();   // table cleared
-        // (the ids were loaded from clamped positions: h >= h1 marks a repeat, not an id)
-        auto count = [&](int id, int h) {
-            const unsigned rel = (unsigned)id - (unsigned)c0;   // negative ids wrap past cn
-            if (h < h1 && rel < (unsigned)cn) {
-                const unsigned owner = (rel / VW) % kThreads;
-                const unsigned slot = (rel / (VW * kThreads)) * VW + rel % VW;
-                atomicAdd(&tab[rel >> 1], 1u << ((rel & 1u) * 16u));
-                atomicOr(&hmask[owner], 1u << slot);
+    if (H > 0) {
+        // Counts the history ids falling in [lo, lo + span) of the chunk and marks their
+        // owners' slots.  The ids were loaded from clamped positions: h >= h1 marks a
+        // repeat, not an id.
+        auto count_part = [&](auto wide, unsigned lo, unsigned span, bool preloaded) {
+            auto count = [&](int id, int h) {
+                const unsigned rel = (unsigned)id - (unsigned)c0;   // negative ids wrap past cn
+                if (h < h1 && rel < (unsigned)cn && rel - lo < span) {
+                    const unsigned owner = (rel / VW) % kThreads;
+                    const unsigned slot = (rel / (VW * kThreads)) * VW + rel % VW;
+                    if constexpr (decltype(wide)::value) atomicAdd(&tab[rel - lo], 1u);
+                    else atomicAdd(&tab[rel >> 1], 1u << ((rel & 1u) * 16u));
+                    atomicOr(&hmask[owner], 1u << slot);
+                }
+            };
+            int hb = h0 + tid;
+            if (preloaded) {
+#pragma unroll
+                for (int j = 0; j < 8; ++j) count(hid[j], hb + j * kThreads);
+                hb += 8 * kThreads;
+            }
+            for (; hb < h1; hb += 8 * kThreads) {
+#pragma unroll
+                for (int j = 0; j < 8; ++j) hid[j] = a.hist_ids[min(hb + j * kThreads, h1 - 1)];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) count(hid[j], hb + j * kThreads);
             }
         };
+        // Penalises the marked elements: rounds of at most kStageLanes owner lanes per
+        // wave spill their registers to the wave's own staging area (a wave's LDS
+        // accesses complete in order), update the marked slots there and reload.
+        auto apply = [&](bool wide, unsigned lo) {
+            const uint32_t mk = hmask[tid];
+            uint64_t pend = __ballot(mk != 0u);
+            float *stage = reinterpret_cast<float *>(raw + ScanLds<E>::stage_off) +
+                           wave_id() * (kStageLanes * ScanLds<E>::stride);
+            const uint64_t below = (1ull << lane_id()) - 1ull;
+            while (pend) {
+                const int rank = __popcll(pend & below);
+                const bool mine = ((pend >> lane_id()) & 1ull) && rank < kStageLanes;
+                if (mine) {
+                    float *sl = stage + rank * ScanLds<E>::stride;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) count(hid[j], h0 + tid + j * kThreads);
-        for (int hb = h0 + tid + 8 * kThreads; hb < h1; hb += 8 * kThreads) {
+                    for (int v = 0; v < E / 4; ++v)
+                        *reinterpret_cast<float4 *>(sl + 4 * v) = make_float4(x[4 * v], x[4 * v + 1], x[4 * v + 2], x[4 * v + 3]);
+                    uint32_t m = mk;
+                    while (m) {
+                        const int e = __builtin_ctz(m);
+                        m &= m - 1u;
+                        const unsigned rel = (unsigned)(((e / VW) * kThreads + tid) * VW + e % VW);
+                        uint32_t c;
+                        if (wide) c = tab[rel - lo];
+                        else c = (tab[rel >> 1] >> ((rel & 1u) * 16u)) & 0xffffu;
+                        sl[e] = penalize(sl[e], c, p);
+                    }
 #pragma unroll
-            for (int j = 0; j < 8; ++j) hid[j] = a.hist_ids[min(hb + j * kThreads, h1 - 1)];
-#pragma unroll
-            for (int j = 0; j < 8; ++j) count(hid[j], hb + j * kThreads);
-        }
-        __syncthreads();
-        const uint32_t mk = hmask[tid];
-        // rounds of at most kStageLanes owner lanes per wave; the staging area is the
-        // wave's own, and a wave's LDS accesses complete in order
-        uint64_t pend = __ballot(mk != 0u);
-        float *stage = reinterpret_cast<float *>(raw + ScanLds<E>::stage_off) +
-                       wave_id() * (kStageLanes * ScanLds<E>::stride);
-        const uint64_t below = (1ull << lane_id()) - 1ull;
-        while (pend) {
-            const int rank = __popcll(pend & below);
-            const bool mine = ((pend >> lane_id()) & 1ull) && rank < kStageLanes;
-            if (mine) {
-                float *sl = stage + rank * ScanLds<E>::stride;
-#pragma unroll
-                for (int v = 0; v < E / 4; ++v)
-                    *reinterpret_cast<float4 *>(sl + 4 * v) = make_float4(x[4 * v], x[4 * v + 1], x[4 * v + 2], x[4 * v + 3]);
-                uint32_t m = mk;
-                while (m) {
-                    const int e = __builtin_ctz(m);
-                    m &= m - 1u;
-                    const int rel = ((e / VW) * kThreads + tid) * VW + e % VW;
-                    sl[e] = penalize(sl[e], (tab[rel >> 1] >> ((rel & 1) * 16)) & 0xffffu, p);
-                }
-#pragma unroll
-                for (int v = 0; v < E / 4; ++v) {
-                    const float4 q = *reinterpret_cast<const float4 *>(sl + 4 * v);
-                    x[4 * v] = q.x; x[4 * v + 1] = q.y; x[4 * v + 2] = q.z; x[4 * v + 3] = q.w;
-                }
-            }
-            pend &= ~__ballot(mine);
-        }
-    } else if (H > 0) {
-        // 32-bit counts over slices of the chunk that fit the table
-        constexpr int RC = ScanLds<E>::value / 4;
-        for (int r0 = 0; r0 < cn; r0 += RC) {
-            for (int i = tid; i < RC; i += kThreads) tab[i] = 0u;
-            __syncthreads();
-            const int lim = min(RC, cn - r0);
-            for (int h = h0 + tid; h < h1; h += kThreads) {
-                const int id = a.hist_ids[h];
-                const unsigned rel = (unsigned)(id - c0 - r0);
-                if (id >= 0 && rel < (unsigned)lim) atomicAdd(&tab[rel], 1u);
-            }
-            __syncthreads();
-#pragma unroll
-            for (int v = 0; v < NV; ++v) {
-#pragma unroll
-                for (int e = 0; e < VW; ++e) {
-                    const unsigned rel = (unsigned)((v * kThreads + tid) * VW + e - r0);
-                    if (rel < (unsigned)RC) {
-                        const uint32_t c = tab[rel];
-                        if (c) x[v * VW + e] = penalize(x[v * VW + e], c, p);
+                    for (int v = 0; v < E / 4; ++v) {
+                        const float4 q = *reinterpret_cast<const float4 *>(sl + 4 * v);
+                        x[4 * v] = q.x; x[4 * v + 1] = q.y; x[4 * v + 2] = q.z; x[4 * v + 3] = q.w;
                     }
                 }
+                pend &= ~__ballot(mine);
             }
+        };
+        // 32-bit counts of half a chunk fill the table: two parts
+        constexpr unsigned kHalf = C / 2;
+        const int parts = packed ? 1 : 2;
+        __syncthreads();   // table cleared
+#pragma unroll 1
+        for (int part = 0; part < parts; ++part) {
+            if (part > 0) {
+                __syncthreads();
+                clear();
+                __syncthreads();
+            }
+            if (packed) count_part(std::false_type{}, 0u, (unsigned)C, true);
+            else count_part(std::true_type{}, part * kHalf, kHalf, part == 0);
             __syncthreads();
+            apply(!packed, part * kHalf);
         }
     }
     if (divided) {

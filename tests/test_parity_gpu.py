@@ -153,6 +153,35 @@ def test_vocab_sizes_and_modes(vocab, dtype):
     check(out, rows, params, probs=True)
 
 
+@pytest.mark.parametrize('dtype', [torch.float32, torch.bfloat16])
+def test_long_histories_count_past_16_bits(dtype):
+    """Histories of 65536 ids or more take 32-bit counts over each half of a chunk in
+    turn; an id repeated more than 65535 times keeps its exact count."""
+    say(f'long histories dtype={dtype}')
+    rng = np.random.default_rng(12)
+    V = 151936
+    kinds = ['greedy', 'topk', 'topp', 'full'] * 2
+    logits = torch.from_numpy((rng.standard_normal((len(kinds), V)) * 2).astype(np.float32)).to(dtype)
+    params = []
+    for i, k in enumerate(kinds):
+        t, tk, tp = {'greedy': (0.0, 0, 1.0), 'topk': (0.8, 50, 1.0), 'topp': (0.9, 0, 0.9),
+                     'full': (1.1, 0, 1.0)}[k]
+        params.append(SamplingParams(temperature=t, top_k=tk, top_p=tp, repetition_penalty=1.2,
+                                     logprobs=3, presence_penalty=0.2, frequency_penalty=2e-5))
+    hist = []
+    for i in range(len(kinds)):
+        hot = int(rng.integers(0, V))
+        h = np.concatenate([np.full(66000 + 1000 * i, hot), rng.integers(0, V, 5000),
+                            rng.integers(0, 64, 3000)])
+        rng.shuffle(h)
+        hist.append(h.tolist())
+    # the hot id's penalty depends on its full count: 66000 * 2e-5 moves it by 1.32
+    u = rng.random(len(kinds)).astype(np.float32)
+    rows = sample_rows(logits, hist, params, u)
+    out = run(logits, params, hist, u, probs=True)
+    check(out, rows, params, probs=True)
+
+
 def test_massive_ties_take_the_row_path():
     say('ties: constant rows')
     V = 50000
