@@ -7,18 +7,19 @@
 //   scan_kernel     grid = B * S workgroups of 256 threads; workgroup (row, chunk)
 //                   loads its chunk of E elements per thread into registers with
 //                   16-byte loads, applies the penalties from an LDS count table of
-//                   the row's history, reduces max / argmax / sum-exp with wave64
+//                   the row's history (owners of history elements penalise them in
+//                   an LDS staging area), reduces max / argmax / sum-exp with wave64
 //                   shuffles, and writes the chunk's candidates: every element at or
-//                   above a lower bound on the chunk's K-th largest value, found by a
-//                   one-wave bisection over the keys of per-thread group maxima.
+//                   above a lower bound on the chunk's K-th largest value, found by
+//                   per-wave ballot bisections over the keys of register-group maxima.
 //   row_kernel      one workgroup per row.  combine_row gathers the row's candidates
-//                   (flattened over chunks), sorts them in LDS (bitonic, <= 2048),
-//                   applies top-k / top-p exactly on them, draws by inverse CDF in
-//                   vocab order, and writes token, logprob and top-N.  Rows the
-//                   candidates cannot settle (top-p mass beyond the candidates, slot
-//                   overflow on massive ties) take dense_resolve: radix selects over
-//                   the whole row (count- and mass-weighted, 8-bit digits, LDS
-//                   histograms).
+//                   (flattened over chunks) into LDS, narrows them with histogram and
+//                   radix selects, rank-sorts the survivors, applies top-k / top-p
+//                   exactly on them, draws by inverse CDF in vocab order, and writes
+//                   token, logprob and top-N.  Rows the candidates cannot settle
+//                   (top-p mass beyond the candidates, slot overflow on massive ties)
+//                   take dense_resolve: radix selects over the whole row (count- and
+//                   mass-weighted, 8-bit digits, LDS histograms).
 //   probs_kernel    optional: the final probability vector of each row.
 //
 // The two main launches are separate kernels on purpose: handing a row to the last
