@@ -84,7 +84,8 @@ bool make_plan(int32_t batch, int32_t vocab, int32_t dtype, int32_t max_top_k, i
     p->off_stats = off;   off = align_up(off + B * S * sizeof(ChunkStat), 256);
     p->off_cands = off;   off = align_up(off + B * S * (size_t)cap * sizeof(Cand), 256);
     p->off_rows = off;    off = align_up(off + B * sizeof(klsample_row_info), 256);
-    p->off_ybuf = off;    off = align_up(off + B * (size_t)vocab * sizeof(float), 256);
+    p->ypitch = (int32_t)align_up((size_t)vocab, 4);   // ybuf rows start 16-byte aligned
+    p->off_ybuf = off;    off = align_up(off + B * (size_t)p->ypitch * sizeof(float), 256);
     p->total = off;
     return (int64_t)batch * p->chunks <= INT32_MAX;
 }
@@ -173,6 +174,7 @@ int klsample_run(const klsample_batch *b, void *stream) {
     a.cands = reinterpret_cast<kls::Cand *>(ws + plan.off_cands);
     a.rows = reinterpret_cast<klsample_row_info *>(ws + plan.off_rows);
     a.ybuf = reinterpret_cast<float *>(ws + plan.off_ybuf);
+    a.ypitch = plan.ypitch;
     a.E = plan.elems;
     a.C = plan.chunk;
     a.S = plan.chunks;

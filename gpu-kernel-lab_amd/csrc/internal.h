@@ -42,6 +42,7 @@ struct Plan {
     int32_t chunk;    // elements per chunk (kThreads * E)
     int32_t chunks;   // chunks per row (S)
     int32_t cand_cap; // candidate slots per chunk
+    int32_t ypitch;   // floats per row of the dense path's score buffer
     size_t off_stats, off_cands, off_rows, off_ybuf, total;
 };
 
@@ -66,7 +67,8 @@ struct Args {
     ChunkStat *stats;
     Cand *cands;           // per (row, chunk): cand_cap slots
     klsample_row_info *rows;
-    float *ybuf;
+    float *ybuf;           // dense row path: per row ypitch final scores
+    int32_t ypitch;        // vocab rounded up to a multiple of 4
     int32_t E, C, S, cand_cap;
     int32_t vec_ok;   // 16-byte vector loads are legal for every row
     int32_t xcd_map;  // place all chunks of a row on one XCD

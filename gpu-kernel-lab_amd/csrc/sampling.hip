@@ -63,6 +63,12 @@ __device__ __forceinline__ float exp_fast(float d) {
     return __builtin_amdgcn_exp2f(d * 1.4426950408889634f);
 }
 
+// Fixed-point weight (unit 2^-40) of a final score y under the row max m: integer sums
+// are exact and independent of their order.
+__device__ __forceinline__ unsigned long long weight_fix(float y, float m) {
+    return (unsigned long long)__double2ull_rn((double)exp_fast(y - m) * kFixScale);
+}
+
 __device__ __forceinline__ int row_mode(const klsample_row_params &p, int V) {
     if (p.flags & KLSAMPLE_ROW_GREEDY) return kGreedy;
     if (p.top_k > 0 && p.top_k < V) return kTopK;
@@ -110,6 +116,15 @@ struct ScanMisc : Red {
     int ncand;
 };
 
+constexpr int kSegCap = 128;   // segments of an ordered search
+
+struct TopPCut {
+    float cut;
+    int cut_idx;             // 0x7fffffff: every entry scoring cut is kept
+    int kept;
+    unsigned long long zf;   // kept mass (fixed point)
+};
+
 struct Misc : Red {
     float rf[2][kWaves];
     int ri[2][kWaves];
@@ -129,6 +144,9 @@ struct Misc : Red {
     int ia, ib;
     uint32_t kmin, kmax;
     double da, db;
+    TopPCut topp;
+    double seg[kSegCap];    // ordered_find: per-segment weight sums
+    int segl[kSegCap];      // ... and last positive item per segment
 };
 
 // ---------------------------------------------------------------------------------
@@ -474,7 +492,7 @@ struct CandSource {
         if (y >= lo) f(fkey(y), (int)e.y, y);
     }
     template <class F>
-    __device__ void each(F f) const {
+    __device__ __forceinline__ void each(F f) const {
         const int lane = lane_id();
         for (int c = wave_id(); c < S; c += 4 * kWaves) {
             uint2 e[4];
@@ -505,7 +523,7 @@ struct LdsSource {
     const unsigned long long *sb;
     int n;
     template <class F>
-    __device__ void each(F f) const {
+    __device__ __forceinline__ void each(F f) const {
         for (int i = threadIdx.x; i < n; i += kThreads) {
             const unsigned long long k = sb[i];
             const uint32_t key = ~(uint32_t)(k >> 32);
@@ -522,11 +540,25 @@ struct DenseSource {
     float cut;
     int cut_idx;
     __device__ __forceinline__ bool keep(float v, int i) const { return v > cut || (v == cut && i <= cut_idx); }
+    // Calls f(key, index, score) for every kept entry.  y is 16-byte aligned and
+    // readable up to V rounded up to 4: eight 16-byte loads are in flight per thread.
     template <class F>
-    __device__ void each(F f) const {
-        for (int i = threadIdx.x; i < V; i += kThreads) {
-            const float v = y[i];
-            if (keep(v, i)) f(fkey(v), i, v);
+    __device__ __forceinline__ void each(F f) const {
+        constexpr int U = 8;
+        const int vlast = (V - 1) & ~3;
+        for (int t0 = 0; t0 < V; t0 += kThreads * 4 * U) {
+            float4 q[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u)
+                q[u] = *reinterpret_cast<const float4 *>(y + min(t0 + (u * kThreads + (int)threadIdx.x) * 4, vlast));
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int i = t0 + (u * kThreads + (int)threadIdx.x) * 4;
+                const float v4[4] = {q[u].x, q[u].y, q[u].z, q[u].w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    if (i + e < V && keep(v4[e], i + e)) f(fkey(v4[e]), i + e, v4[e]);
+            }
         }
     }
 };
@@ -591,7 +623,7 @@ struct MassPick {
 };
 
 template <typename Src>
-__device__ __forceinline__ bool select_mass(const Src &src, double target, double m, MassPick &out, Misc &ms) {
+__device__ __forceinline__ bool select_mass(const Src &src, double target, float m, MassPick &out, Misc &ms) {
     uint32_t prefix = 0u;
     unsigned long long above = 0ull;
     uint32_t above_count = 0u;
@@ -602,9 +634,8 @@ __device__ __forceinline__ bool select_mass(const Src &src, double target, doubl
         src.each([&](uint32_t key, int, float v) {
             if ((key & hmask) == prefix) {
                 const uint32_t b = (key >> shift) & 255u;
-                const double w = exp((double)v - m);
                 atomicAdd(&ms.hist[b], 1u);
-                atomicAdd(&ms.hmass[b], (unsigned long long)__double2ull_rn(w * kFixScale));
+                atomicAdd(&ms.hmass[b], weight_fix(v, m));
             }
         });
         __syncthreads();
@@ -656,47 +687,166 @@ __device__ __forceinline__ bool select_mass(const Src &src, double target, doubl
     return true;
 }
 
-// Walk items [0, n) in order; `weight(i)` >= 0.  Returns the first item whose
-// inclusive cumulative weight exceeds `target`, or -1; `last` receives the last item
-// with positive weight (-1 if none).
+// Walk items [0, n) in order; `weight(i)` >= 0 (a pure function of i).  Returns the
+// first item whose inclusive cumulative weight exceeds `target`, or -1; `last`
+// receives the last item with positive weight (-1 if none) and `before` the weight
+// before the returned item (the total if none).  Three steps: per-segment sums (one
+// wave per segment, lanes strided, eight weights in flight per lane), the crossing
+// segment (one wave scan), and inside it runs of eight items per lane.
 template <typename W>
 __device__ __forceinline__ int ordered_find(int n, W weight, double target, Misc &ms, int &last, double &before) {
-    double base = 0.0;
-    int lastp = -1;
-    for (int t0 = 0; t0 < n; t0 += kThreads * 4) {
-        const int i0 = t0 + 4 * (int)threadIdx.x;
-        double w[4], s = 0.0;
+    int seg = 2048;
+    while ((n + seg - 1) / seg > kSegCap) seg *= 2;
+    const int nseg = (n + seg - 1) / seg;
+    const int lane = lane_id();
+    if (nseg <= 1) {
+        // one segment: the run walk alone
+        if (wave_id() == 0) {
+            double base = 0.0, bf = 0.0;
+            int found = -1, lastp = -1;
+            for (int r0 = 0; r0 < n && found < 0; r0 += 64 * 8) {
+                const int l0 = r0 + 8 * lane;
+                double wv[8], ls = 0.0;
+                int lp = -1;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) { w[j] = (i0 + j < n) ? weight(i0 + j) : 0.0; s += w[j]; }
-        double tot;
-        const double ex = block_excl_scan(s, ms.red.d, tot);
-        double c = base + ex;
-        int loc = 0x7fffffff, lp = -1;
-        double cb = 0.0;
+                for (int j = 0; j < 8; ++j) {
+                    const double x = weight(min(l0 + j, n - 1));
+                    wv[j] = (l0 + j < n) ? x : 0.0;
+                    ls += wv[j];
+                    if (wv[j] > 0.0) lp = l0 + j;
+                }
+                lastp = max(lastp, wave_reduce(lp, OpMaxI(), -1));
+                const double incl = wave_incl_scan(ls);
+                const double ex = wave_shift_excl(incl);
+                const unsigned long long bal = __ballot(base + ex + ls > target);
+                if (bal != 0ull) {
+                    const int fl = __ffsll((long long)bal) - 1;
+                    int f = -1;
+                    double c = base + ex, cb = 0.0;
+                    if (lane == fl) {
+                        int lpos = -1;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            if (w[j] > 0.0) {
-                if (loc == 0x7fffffff && c + w[j] > target) { loc = i0 + j; cb = c; }
-                c += w[j];
-                lp = i0 + j;
+                        for (int j = 0; j < 8; ++j) {
+                            if (wv[j] > 0.0) {
+                                if (f < 0 && c + wv[j] > target) { f = l0 + j; cb = c; }
+                                if (f < 0) c += wv[j];
+                                lpos = l0 + j;
+                            }
+                        }
+                        if (f < 0) { f = lpos; cb = c; }
+                    }
+                    found = readlane(f, fl);
+                    bf = readlane(cb, fl);
+                } else {
+                    base += readlane(incl, 63);
+                }
+            }
+            if (lane == 0) { ms.ib = found; ms.db = found < 0 ? base : bf; ms.last = lastp; }
+        }
+        __syncthreads();
+        const int found = ms.ib;
+        before = ms.db;
+        last = ms.last;
+        __syncthreads();
+        return found;
+    }
+    for (int sg = wave_id(); sg < nseg; sg += kWaves) {
+        const int b0 = sg * seg, b1 = min(n, b0 + seg);
+        double sum = 0.0;
+        int lp = -1;
+        for (int i0 = b0; i0 < b1; i0 += 64 * 8) {
+            double wv[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int i = i0 + j * 64 + lane;
+                const double x = weight(min(i, b1 - 1));
+                wv[j] = (i < b1) ? x : 0.0;
+            }
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                sum += wv[j];
+                if (wv[j] > 0.0) lp = i0 + j * 64 + lane;
             }
         }
-        const int found = block_min(loc, ms);
-        lp = block_maxi(lp, ms);
-        if (lp >= 0) lastp = lp;
-        if (found != 0x7fffffff) {
-            if (loc == found) ms.da = cb;
-            __syncthreads();
-            before = ms.da;
-            last = lastp;
-            __syncthreads();
-            return found;
-        }
-        base += tot;
+        sum = wave_reduce(sum, OpSumD(), 0.0);
+        lp = wave_reduce(lp, OpMaxI(), -1);
+        if (lane == 0) { ms.seg[sg] = sum; ms.segl[sg] = lp; }
     }
-    last = lastp;
-    before = base;
-    return -1;
+    __syncthreads();
+    if (wave_id() == 0) {
+        const int s0 = 2 * lane, s1 = 2 * lane + 1;
+        const double a0 = s0 < nseg ? ms.seg[s0] : 0.0, a1 = s1 < nseg ? ms.seg[s1] : 0.0;
+        const int lp = max(s0 < nseg ? ms.segl[s0] : -1, s1 < nseg ? ms.segl[s1] : -1);
+        const double incl = wave_incl_scan(a0 + a1);
+        const double ex = wave_shift_excl(incl);
+        const bool c0 = s0 < nseg && ex + a0 > target;
+        const bool c1 = s1 < nseg && (ex + a0) + a1 > target;
+        const unsigned long long bal = __ballot(c0 || c1);
+        const int lpm = wave_reduce(lp, OpMaxI(), -1);
+        if (bal == 0ull) {
+            if (lane == 0) { ms.ia = -1; ms.da = 0.0; }
+            if (lane == 63) ms.db = incl;
+        } else if (lane == __ffsll((long long)bal) - 1) {
+            ms.ia = c0 ? s0 : s1;
+            ms.da = c0 ? ex : ex + a0;
+        }
+        if (lane == 0) ms.last = lpm;
+    }
+    __syncthreads();
+    const int sg = ms.ia;
+    last = ms.last;
+    if (sg < 0) {
+        before = ms.db;
+        __syncthreads();
+        return -1;
+    }
+    if (wave_id() == 0) {
+        const int b0 = sg * seg, b1 = min(n, b0 + seg);
+        double base = ms.da;
+        int found = -1;
+        double bf = 0.0;
+        for (int r0 = b0; r0 < b1 && found < 0; r0 += 64 * 8) {
+            const int l0 = r0 + 8 * lane;
+            double wv[8], ls = 0.0;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const double x = weight(min(l0 + j, b1 - 1));
+                wv[j] = (l0 + j < b1) ? x : 0.0;
+                ls += wv[j];
+            }
+            const double incl = wave_incl_scan(ls);
+            const double ex = wave_shift_excl(incl);
+            const unsigned long long bal = __ballot(base + ex + ls > target);
+            if (bal != 0ull) {
+                const int fl = __ffsll((long long)bal) - 1;
+                int f = -1;
+                double c = base + ex, cb = 0.0;
+                if (lane == fl) {
+                    int lpos = -1;
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) {
+                        if (wv[j] > 0.0) {
+                            if (f < 0 && c + wv[j] > target) { f = l0 + j; cb = c; }
+                            if (f < 0) c += wv[j];
+                            lpos = l0 + j;
+                        }
+                    }
+                    if (f < 0) { f = lpos; cb = c; }   // rounding: the run's sum crossed, its items did not
+                }
+                found = readlane(f, fl);
+                bf = readlane(cb, fl);
+            } else {
+                base += readlane(incl, 63);
+            }
+        }
+        if (found < 0) { found = ms.segl[sg]; bf = base; }   // rounding: no item of the segment crossed
+        if (lane == 0) { ms.ib = found; ms.db = bf; }
+    }
+    __syncthreads();
+    const int found = ms.ib;
+    before = ms.db;
+    __syncthreads();
+    return found;
 }
 
 // Bitonic sort (ascending) of n = power of two 64-bit keys in LDS.
@@ -921,26 +1071,175 @@ __device__ __forceinline__ int dense_topn(const DenseSource &src, int N, unsigne
     return want;
 }
 
+// Top-p cut over a dense source by a mass histogram in log space: bin b holds the
+// kept entries with (m - y) * 64 in [b, b + 1) (the last bin everything further
+// down), which orders bins like scores.  The bin where the running mass from the top
+// first exceeds `target` is gathered into LDS, sorted, and walked to the first group
+// of equal scores whose mass crosses; ties in that group are kept in index order as
+// far as the remaining mass allows.  Returns 1 with the cut, 0 if the whole source's
+// mass does not exceed `target` (everything kept), -1 if the bin is the last one or
+// too large for LDS (the caller falls back to the radix selection).  zk / nk receive
+// the source's total mass and finite count either way (except -1).
+constexpr int kMassBins = 2048;
+
+__device__ __forceinline__ int topp_cut_bins(const DenseSource &src, float m, float top_p, unsigned char *raw,
+                                             int cap, unsigned long long &zk, int &nk, TopPCut &out, Misc &ms) {
+    uint32_t *hn = reinterpret_cast<uint32_t *>(raw);
+    unsigned long long *hw = reinterpret_cast<unsigned long long *>(raw + kMassBins * 4);
+    for (int i = threadIdx.x; i < kMassBins; i += kThreads) { hn[i] = 0u; hw[i] = 0ull; }
+    if (threadIdx.x == 0) { ms.ncand = 0; ms.flag = 0; }
+    __syncthreads();
+    auto bin = [m](float y) -> int {
+        const float d = (m - y) * 64.0f;
+        return d < (float)(kMassBins - 1) ? (int)d : kMassBins - 1;
+    };
+    src.each([&](uint32_t, int, float y) {
+        if (y > kNegInf) {
+            const int b = bin(y);
+            atomicAdd(&hn[b], 1u);
+            atomicAdd(&hw[b], weight_fix(y, m));
+        }
+    });
+    __syncthreads();
+    if (wave_id() == 0) {
+        // 32 consecutive bins per lane
+        const int l = lane_id();
+        unsigned long long ws = 0ull;
+        uint32_t cs = 0u;
+#pragma unroll 8
+        for (int j = 0; j < kMassBins / 64; ++j) { ws += hw[l * (kMassBins / 64) + j]; cs += hn[l * (kMassBins / 64) + j]; }
+        const unsigned long long wi = wave_incl_scan(ws);
+        const uint32_t ci = wave_incl_scan(cs);
+        const unsigned long long total = readlane(wi, 63);
+        const double target = (double)top_p * (double)total;
+        const unsigned long long bal = __ballot((double)wi > target);
+        const uint32_t ctotal = readlane(ci, 63);
+        if (l == 0) { ms.sel_above_mass = total; ms.sel_need = ctotal; }
+        if (bal != 0ull && l == __ffsll((long long)bal) - 1) {
+            unsigned long long acc = wi - ws;
+            uint32_t nacc = ci - cs;
+            for (int j = 0; j < kMassBins / 64; ++j) {
+                const int b = l * (kMassBins / 64) + j;
+                if ((double)(acc + hw[b]) > target) {
+                    ms.sel_digit = (uint32_t)b;
+                    ms.hmass[0] = acc;          // mass above the bin
+                    ms.sel_above_count = nacc;  // entries above the bin
+                    ms.ib = (int)hn[b];         // entries in the bin
+                    ms.flag = 1;
+                    break;
+                }
+                acc += hw[b];
+                nacc += hn[b];
+            }
+        }
+    }
+    __syncthreads();
+    zk = ms.sel_above_mass;
+    nk = (int)ms.sel_need;
+    if (!ms.flag) { __syncthreads(); return 0; }
+    const int bs = (int)ms.sel_digit, nb = ms.ib;
+    const unsigned long long above = ms.hmass[0];
+    const uint32_t above_count = ms.sel_above_count;
+    __syncthreads();
+    if (bs == kMassBins - 1 || nb > cap) return -1;
+    // the bin's entries, sorted best first
+    unsigned long long *G = reinterpret_cast<unsigned long long *>(raw);
+    src.each([&](uint32_t, int idx, float y) {
+        if (y > kNegInf && bin(y) == bs) {
+            const int pos = wave_append(&ms.ncand);
+            if (pos < cap) G[pos] = desc_key(y, idx);
+        }
+    });
+    __syncthreads();
+    const int n = min(ms.ncand, cap);
+    sort_keys(G, n);
+    if (wave_id() == 0) {
+        const double target = (double)top_p * (double)zk;
+        const int l = lane_id();
+        unsigned long long run = above;
+        int j = -1;
+        unsigned long long incl_j = 0ull;
+        for (int i0 = 0; i0 < n && j < 0; i0 += 64) {
+            const int i = i0 + l;
+            const unsigned long long w = i < n ? weight_fix(desc_key_y(G[i]), m) : 0ull;
+            const unsigned long long incl = run + wave_incl_scan(w);
+            const unsigned long long bal = __ballot(i < n && (double)incl > target);
+            if (bal != 0ull) {
+                const int fl = __ffsll((long long)bal) - 1;
+                j = i0 + fl;
+                incl_j = readlane(incl, fl);
+            }
+            run = readlane(incl, 63);
+        }
+        if (j < 0) j = n - 1, incl_j = run;   // rounding: take the bin's last entry
+        // the group of equal scores around j: [gs, ge)
+        const float yg = desc_key_y(G[j]);
+        const unsigned long long kg = (unsigned long long)(~fkey(yg)) << 32;
+        int lo = 0, hi = j;
+        while (lo < hi) { const int mid = (lo + hi) >> 1; if (G[mid] < kg) lo = mid + 1; else hi = mid; }
+        const int gs = lo;
+        lo = j + 1; hi = n;
+        while (lo < hi) { const int mid = (lo + hi) >> 1; if ((G[mid] >> 32) == (kg >> 32)) lo = mid + 1; else hi = mid; }
+        const int ge = lo;
+        const unsigned long long wt = weight_fix(yg, m);
+        const unsigned long long above_g = incl_j - (unsigned long long)(j - gs + 1) * wt;
+        const int count = ge - gs;
+        int keep = count;
+        if (wt > 0ull) {
+            const double room = target - (double)above_g;
+            const double k = floor(room / (double)wt) + 1.0;
+            keep = (int)fmin((double)count, fmax(1.0, k));
+        }
+        if (l == 0) {
+            out.cut = yg;
+            out.cut_idx = (keep < count) ? desc_key_idx(G[gs + keep - 1]) : 0x7fffffff;
+            out.kept = (int)above_count + gs + keep;
+            out.zf = above_g + (unsigned long long)keep * wt;
+            ms.topp = out;
+        }
+    }
+    __syncthreads();
+    out = ms.topp;
+    __syncthreads();
+    return 1;
+}
+
 // Multi-pass row path: materialise the row's final scores in the workspace, then
-// resolve top-k / top-p / the draw / top-N with radix selects over the whole row.
-// Taken when the chunk candidates cannot settle the row.
+// resolve top-k / top-p / the draw / top-N over the whole row.  Taken when the chunk
+// candidates cannot settle the row.
 template <typename TIn, int E>
 __device__ __forceinline__ void dense_resolve(const Args &a, int row, const klsample_row_params &p, int mode,
                               unsigned char *raw, Misc &ms) {
     constexpr int C = kThreads * E;
     const int V = a.V;
-    float *yb = a.ybuf + (size_t)row * V;
+    float *yb = a.ybuf + (size_t)row * a.ypitch;
     const bool pen = has_penalty(a, p, row);
     uint32_t *cnt = reinterpret_cast<uint32_t *>(raw);
     float mt = kNegInf;
     int at = 0x7fffffff;
+    const TIn *src = reinterpret_cast<const TIn *>(a.logits) + (int64_t)row * a.row_stride;
     for (int c = 0; c < a.S; ++c) {
         const int c0 = c * C, cn = min(C, V - c0);
         if (pen) build_counts<C>(cnt, a, row, c0, cn);
-        for (int i = threadIdx.x; i < cn; i += kThreads) {
-            const float y = element_final<TIn>(a, p, row, c0 + i, pen ? cnt : nullptr, c0, mode != kGreedy);
-            yb[c0 + i] = y;
-            if (y > mt) { mt = y; at = c0 + i; }
+        // eight loads in flight per thread
+        for (int i0 = 0; i0 < cn; i0 += kThreads * 8) {
+            float x[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) x[j] = Loader<TIn>::one(src + c0 + min(i0 + j * kThreads + (int)threadIdx.x, cn - 1));
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int i = i0 + j * kThreads + (int)threadIdx.x;
+                if (i < cn) {
+                    float y = x[j];
+                    if (pen) {
+                        const uint32_t k = cnt[i];
+                        if (k) y = penalize(y, k, p);
+                    }
+                    if (mode != kGreedy) y = __fdiv_rn(y, p.temperature);
+                    yb[c0 + i] = y;
+                    if (y > mt) { mt = y; at = c0 + i; }
+                }
+            }
         }
         __syncthreads();
     }
@@ -949,9 +1248,7 @@ __device__ __forceinline__ void dense_resolve(const Args &a, int row, const klsa
     if (arg == 0x7fffffff) arg = 0;
     __syncthreads();
     const double md = (double)m;
-    auto wfix = [md](float y) -> unsigned long long {
-        return (unsigned long long)__double2ull_rn(exp((double)y - md) * kFixScale);
-    };
+    auto wfix = [m](float y) -> unsigned long long { return weight_fix(y, m); };
     unsigned long long *sortbuf = reinterpret_cast<unsigned long long *>(raw);
     RowOut r;
     r.m = m;
@@ -977,16 +1274,32 @@ __device__ __forceinline__ void dense_resolve(const Args &a, int row, const klsa
         const DenseSource ge{yb, V, lo, V};
         unsigned long long zk = 0ull;
         int nk = 0;
-        ge.each([&](uint32_t, int, float y) { zk += wfix(y); nk += (y > kNegInf) ? 1 : 0; });
-        zk = block_sumq(zk, ms);
-        nk = block_sum(nk, ms);
         float cut = lo;
-        int cut_idx = V, kept = nk;
-        unsigned long long zf = zk;
+        int cut_idx = V, kept = 0;
+        unsigned long long zf = 0ull;
+        int how = -1;   // top-p by mass bins: 1 cut, 0 nothing removed, -1 not settled
         if (p.flags & KLSAMPLE_ROW_TOP_P) {
+            TopPCut tc;
+            how = topp_cut_bins(ge, m, p.top_p, raw, 2 * kSortCap, zk, nk, tc, ms);
+            if (how == 1) {
+                cut = tc.cut;
+                cut_idx = tc.cut_idx == 0x7fffffff ? V : tc.cut_idx;
+                kept = tc.kept;
+                zf = tc.zf;
+            }
+        } else {
+            ge.each([&](uint32_t, int, float y) { zk += wfix(y); nk += (y > kNegInf) ? 1 : 0; });
+            zk = block_sumq(zk, ms);
+            nk = block_sum(nk, ms);
+        }
+        if (how != 1) {
+            kept = nk;
+            zf = zk;
+        }
+        if (how < 0 && (p.flags & KLSAMPLE_ROW_TOP_P)) {
             const double target = (double)p.top_p * (double)zk;
             MassPick mp;
-            if (select_mass(ge, target, md, mp, ms)) {
+            if (select_mass(ge, target, m, mp, ms)) {
                 const unsigned long long wt = mp.group_count ? mp.group_mass / mp.group_count : 0ull;
                 uint32_t keep = mp.group_count;
                 if (wt > 0ull) {
