@@ -2226,6 +2226,26 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(E >= 3
         // full chunk: every 16-byte load issued back to back
 #pragma unroll
         for (int v = 0; v < NV; ++v) Loader<TIn>::vec(src + (v * kThreads + tid) * VW, &x[v * VW]);
+    } else if (a.vec_ok && cn >= VW) {
+        // partial chunk: the same loads with addresses clamped to the last whole vector
+        // (never predicated, so they stay in flight together), positions past cn
+        // masked; the one vector straddling cn is re-read element by element
+        const int lastfull = (cn / VW - 1) * VW;
+#pragma unroll
+        for (int v = 0; v < NV; ++v) Loader<TIn>::vec(src + min((v * kThreads + tid) * VW, lastfull), &x[v * VW]);
+#pragma unroll
+        for (int v = 0; v < NV; ++v) {
+            const int li = (v * kThreads + tid) * VW;
+#pragma unroll
+            for (int e = 0; e < VW; ++e) x[v * VW + e] = (li + e < cn) ? x[v * VW + e] : kNegInf;
+            if (li < cn && li + VW > cn) {
+#pragma unroll
+                for (int e = 0; e < VW; ++e) {
+                    const float t = Loader<TIn>::one(src + min(li + e, cn - 1));
+                    x[v * VW + e] = (li + e < cn) ? t : kNegInf;
+                }
+            }
+        }
     } else {
 #pragma unroll
         for (int v = 0; v < NV; ++v) {
