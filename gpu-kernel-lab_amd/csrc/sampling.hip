@@ -114,6 +114,10 @@ struct ScanMisc : Red {
     uint32_t wbound[kWaves];
     uint32_t bound_key;
     int ncand;
+    // per-wave max, sum of exp relative to it, finite count and lowest argmax
+    float wm[kWaves];
+    double wz[kWaves];
+    int wn[kWaves], wa[kWaves];
 };
 
 constexpr int kSegCap = 128;   // segments of an ordered search
@@ -2352,34 +2356,40 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(E >= 3
     st.overflow = 0;
     st.nfinite = 0;
     if (mode != kTopK) {
+        // per wave (no barrier): max, lowest argmax, sum of exp relative to the wave's
+        // max, finite count; thread 0 combines the waves after a later barrier
         float mt = kNegInf;
 #pragma unroll
         for (int e = 0; e < E; ++e) mt = fmaxf(mt, x[e]);
-        const float m = block_max(mt, ms);
+        const float mw = wave_reduce(mt, OpMaxF(), kNegInf);
+        int at = 0x7fffffff;
         if (mode == kGreedy) {
-            int at = 0x7fffffff;
 #pragma unroll
             for (int v = 0; v < NV; ++v) {
                 const int li = (v * kThreads + tid) * VW;
 #pragma unroll
                 for (int e = 0; e < VW; ++e)
-                    if (x[v * VW + e] == m && li + e < cn && li + e < at) at = li + e;
+                    if (x[v * VW + e] == mw && li + e < cn && li + e < at) at = li + e;
             }
-            at = block_min(at, ms);
-            st.arg = (at == 0x7fffffff) ? 0x7fffffff : c0 + at;
+            at = wave_reduce(at, OpMinI(), 0x7fffffff);
         }
         double z = 0.0;
         int nfin = 0;
-        if (m > kNegInf) {
+        if (mw > kNegInf) {
 #pragma unroll
             for (int e = 0; e < E; ++e) {
-                z += (double)exp_fast(x[e] - m);
+                z += (double)exp_fast(x[e] - mw);
                 nfin += (x[e] > kNegInf) ? 1 : 0;
             }
         }
-        st.z = block_sumd(z, ms);
-        st.nfinite = block_sum(nfin, ms);
-        st.m = m;
+        z = wave_reduce(z, OpSumD(), 0.0);
+        nfin = wave_reduce(nfin, OpSumI(), 0);
+        if (lane_id() == 0) {
+            ms.wm[wave_id()] = mw;
+            ms.wz[wave_id()] = z;
+            ms.wn[wave_id()] = nfin;
+            ms.wa[wave_id()] = at;
+        }
     }
 
     const int K = (mode == kGreedy || mode == kFull) ? a.N
@@ -2409,6 +2419,10 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(E >= 3
         if (lane_id() == 0 && wtot > 0) wbase = atomicAdd(&ms.ncand, wtot);
         wbase = readlane(wbase, 0);
         int pos = wbase + incl - my;
+        // every wave has reserved its run: the total is known before any store, so no
+        // barrier waits for the stores
+        __syncthreads();
+        const int total = ms.ncand;
         // scores are written as streamed: top-k rows in the penalised space (the row
         // kernel divides by T), the others in final space
         Cand *out = a.cands + ((size_t)row * a.S + chunk) * a.cand_cap;
@@ -2430,11 +2444,31 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(E >= 3
                 }
             }
         }
+        st.ncand = min(total, cap);
+        st.overflow = total > cap ? 1 : 0;
+    } else {
         __syncthreads();
-        st.ncand = min(ms.ncand, cap);
-        st.overflow = ms.ncand > cap ? 1 : 0;
     }
-    if (tid == 0) a.stats[(size_t)row * a.S + chunk] = st;
+    if (tid == 0) {
+        if (mode != kTopK) {
+            float m = ms.wm[0];
+#pragma unroll
+            for (int w = 1; w < kWaves; ++w) m = fmaxf(m, ms.wm[w]);
+            double z = 0.0;
+            int nfin = 0, at = 0x7fffffff;
+#pragma unroll
+            for (int w = 0; w < kWaves; ++w) {
+                if (ms.wm[w] > kNegInf) z += ms.wz[w] * (double)exp_fast(ms.wm[w] - m);
+                nfin += ms.wn[w];
+                if (ms.wm[w] == m) at = min(at, ms.wa[w]);
+            }
+            st.m = m;
+            st.z = z;
+            st.nfinite = nfin;
+            if (mode == kGreedy) st.arg = (at == 0x7fffffff) ? 0x7fffffff : c0 + at;
+        }
+        a.stats[(size_t)row * a.S + chunk] = st;
+    }
 }
 
 template <int C>
