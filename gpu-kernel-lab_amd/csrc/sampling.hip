@@ -440,18 +440,18 @@ __device__ __forceinline__ float block_group_bound_dispatch(const float (&x)[E],
     return kNegInf;
 }
 
-// The chunk bound (-inf: keep every element).  Full chunks take the per-wave bound:
-// groups start as coarse as 4*Kw groups per wave allow and a wave refines them while
-// fewer than Kw hold a finite element.  A partial chunk, or a wave still short of Kw
-// finite groups (masked or massively tied scores), takes one bound over the whole
-// chunk instead.  `keys` holds kThreads * min(E, 16) words of LDS.  Ends with a barrier.
+// The chunk bound (-inf: keep every element).  Each wave takes its own bound: groups
+// start as coarse as 4*Kw groups per wave allow and a wave refines them while fewer
+// than Kw hold a finite element (positions past the end of a partial chunk are -inf).
+// If a wave is still short of Kw finite groups (a short chunk, masked or massively
+// tied scores), one bound over the whole chunk is taken instead.  `keys` holds
+// kThreads * min(E, 16) words of LDS.  Ends with a barrier.
 template <int E>
 __device__ __forceinline__ float chunk_bound(const float (&x)[E], int K, int cn, uint32_t *keys, ScanMisc &ms) {
     constexpr int kMaxG = E < 16 ? E : 16;
-    constexpr int C = kThreads * E;
     const int Kw = (K + kWaves - 1) / kWaves;
     uint32_t t = 0u;
-    if (cn == C && Kw <= 64 * kMaxG) {
+    if (Kw <= 64 * kMaxG) {
         int G = 1;
         while (G < kMaxG && 64 * G < 4 * Kw) G <<= 1;
         t = wave_group_bound_dispatch<E>(x, G, Kw);
@@ -1803,11 +1803,11 @@ __device__ __forceinline__ bool combine_row(const Args &a, int row, const klsamp
     const Cand *rc = a.cands + (size_t)row * S * a.cand_cap;
 
     // 1. The chunk summaries and the first candidate pairs of the first chunks, requested
-    //    together: one memory round trip for the common row.
-    const bool want_cands = !((mode == kGreedy || mode == kFull) && N == 0);
+    //    together and independently of the row's parameters: one memory round trip for
+    //    the common row.  (Greedy and full rows without top-N read slots they ignore.)
     const int ppc = min(a.cand_cap / 2, kSpecPairs);   // a power of two
     const int pshift = 31 - __clz(ppc);
-    const int nspec = want_cands ? min(S, (kSpecLoads * kThreads) >> pshift) : 0;
+    const int nspec = min(S, (kSpecLoads * kThreads) >> pshift);
     // (addresses are clamped into range rather than the loads predicated: a predicated
     // load would be waited for before the next one is issued)
     uint4 spec[kSpecLoads];
@@ -1864,12 +1864,12 @@ __device__ __forceinline__ bool combine_row(const Args &a, int row, const klsamp
     if (mode != kTopK) {
         if (has) {
             if (mode == kGreedy && s0.m == m) arg = s0.arg;
-            if (s0.m > kNegInf) Z += s0.z * exp((double)s0.m - (double)m);
+            if (s0.m > kNegInf) Z += s0.z * (double)exp_fast(s0.m - m);
         }
         for (int c = tid + kThreads; c < S; c += kThreads) {
             const ChunkStat s = st[c];
             if (mode == kGreedy && s.m == m) arg = min(arg, s.arg);
-            if (s.m > kNegInf) Z += s.z * exp((double)s.m - (double)m);
+            if (s.m > kNegInf) Z += s.z * (double)exp_fast(s.m - m);
         }
     }
 
