@@ -1712,21 +1712,52 @@ __device__ __forceinline__ int hist_gather(const unsigned long long *A, int n, i
     return ms.ib;
 }
 
+// Ranks of the keys a lane holds (J of them) among sb[0..n): one pass of broadcast
+// reads, two keys per read, compared with all J keys.
+template <int J>
+__device__ __forceinline__ void rank_of_multi(const unsigned long long *sb, int n, const unsigned long long (&mine)[J],
+                                              int (&rank)[J]) {
+#pragma unroll
+    for (int k = 0; k < J; ++k) rank[k] = 0;
+#pragma unroll 4
+    for (int j = 0; j < n; j += 2) {
+        const ulonglong2 q = *reinterpret_cast<const ulonglong2 *>(&sb[j]);
+        const bool second = j + 1 < n;
+#pragma unroll
+        for (int k = 0; k < J; ++k) {
+            rank[k] += (q.x < mine[k]) ? 1 : 0;
+            rank[k] += (second && q.y < mine[k]) ? 1 : 0;
+        }
+    }
+}
+
 // One wave: sort D[0..t) (t <= 256, distinct keys) ascending, up to four keys per lane.
 __device__ __forceinline__ void wave_rank_sort(unsigned long long *D, int t) {
     const int l = lane_id();
-    unsigned long long key[4];
-    int rk[4];
+    if (t <= 64) {
+        const unsigned long long k1[1] = {l < t ? D[l] : ~0ull};
+        int r1[1];
+        rank_of_multi<1>(D, t, k1, r1);
+        __builtin_amdgcn_wave_barrier();
+        if (l < t) D[r1[0]] = k1[0];
+    } else if (t <= 128) {
+        const unsigned long long k2[2] = {D[l], l + 64 < t ? D[l + 64] : ~0ull};
+        int r2[2];
+        rank_of_multi<2>(D, t, k2, r2);
+        __builtin_amdgcn_wave_barrier();
+        D[r2[0]] = k2[0];
+        if (l + 64 < t) D[r2[1]] = k2[1];
+    } else {
+        unsigned long long k4[4];
+        int r4[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int i = l + 64 * j;
-        key[j] = i < t ? D[i] : ~0ull;
-        rk[j] = i < t ? rank_of(D, t, key[j]) : 0;
+        for (int j = 0; j < 4; ++j) k4[j] = l + 64 * j < t ? D[l + 64 * j] : ~0ull;
+        rank_of_multi<4>(D, t, k4, r4);
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            if (l + 64 * j < t) D[r4[j]] = k4[j];
     }
-    __builtin_amdgcn_wave_barrier();
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-        if (l + 64 * j < t) D[rk[j]] = key[j];
     __builtin_amdgcn_wave_barrier();
 }
 
