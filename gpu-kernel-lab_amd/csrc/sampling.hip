@@ -133,6 +133,7 @@ struct Misc : Red {
     float rf[2][kWaves];
     int ri[2][kWaves];
     uint32_t hist[256];
+    uint32_t part[kThreads];   // block_rank_sort: per-thread partial ranks
     unsigned long long hmass[256];
     int topn_idx[kMaxLogprobs];
     float topn_y[kMaxLogprobs];
@@ -929,11 +930,42 @@ __device__ __forceinline__ void rank_sort(unsigned long long *sb, int n) {
     __syncthreads();
 }
 
+// Sort sb[0..n) (distinct keys, 2 <= n <= kThreads) ascending with the whole block:
+// the kThreads / n threads given to a key each count the keys below it in one slice of
+// sb (broadcast 16-byte reads), and the slices' counts are added.  `part` holds
+// kThreads ints of LDS.  Three barriers.
+__device__ __forceinline__ void block_rank_sort(unsigned long long *sb, int n, uint32_t *part) {
+    const int tid = threadIdx.x;
+    const int segs = kThreads / n;
+    const int k = tid % n, sg = tid / n;
+    const int len = (((n + segs - 1) / segs) + 1) & ~1;   // even: slices start 16-byte aligned
+    unsigned long long key = ~0ull;
+    uint32_t cnt = 0u;
+    if (sg < segs) {
+        key = sb[k];
+        const int j0 = sg * len, j1 = min(n, j0 + len);
+#pragma unroll 4
+        for (int j = j0; j < j1; j += 2) {
+            const ulonglong2 q = *reinterpret_cast<const ulonglong2 *>(&sb[j]);
+            cnt += (q.x < key) ? 1u : 0u;
+            cnt += (j + 1 < j1 && q.y < key) ? 1u : 0u;
+        }
+    }
+    part[tid] = cnt;
+    __syncthreads();
+    int rank = 0;
+    if (tid < n)
+        for (int g = 0; g < segs; ++g) rank += (int)part[g * n + tid];
+    __syncthreads();
+    if (tid < n) sb[rank] = key;
+    __syncthreads();
+}
+
 // Sort n distinct keys ascending in LDS (capacity >= pow2_ceil(n)).
-__device__ __forceinline__ void sort_keys(unsigned long long *sb, int n) {
+__device__ __forceinline__ void sort_keys(unsigned long long *sb, int n, uint32_t *part) {
     if (n <= 1) return;
     if (n <= kThreads) {
-        rank_sort(sb, n);
+        block_rank_sort(sb, n, part);
         return;
     }
     const int n2 = pow2_ceil(n);
@@ -1156,7 +1188,7 @@ __device__ __forceinline__ int topp_cut_bins(const DenseSource &src, float m, fl
     });
     __syncthreads();
     const int n = min(ms.ncand, cap);
-    sort_keys(G, n);
+    sort_keys(G, n, ms.part);
     if (wave_id() == 0) {
         const double target = (double)top_p * (double)zk;
         const int l = lane_id();
@@ -1390,7 +1422,7 @@ __device__ __forceinline__ void finish_sampled(const Args &a, int row, int mode,
         D[i] = ((unsigned long long)(uint32_t)desc_key_idx(k) << 32) | __float_as_uint(desc_key_y(k));
     }
     __syncthreads();
-    sort_keys(D, L);
+    sort_keys(D, L, ms.part);
     int last;
     double before;
     int j = ordered_find(
@@ -1427,22 +1459,9 @@ __device__ __forceinline__ int topp_prefix(const unsigned long long *D, int n, d
 // ---------------------------------------------------------------------------------
 // One-wave finish of a row whose kept set is small: no barriers, one key per lane.
 
-// Sort D[0..n) ascending (best first) in LDS: one wave ranks n <= 64 keys (the LDS
-// operations of one wave complete in order, so its reads precede its writes), else the
-// block.
-__device__ __forceinline__ void sort_top(unsigned long long *D, int n) {
-    if (n <= 64) {
-        if (wave_id() == 0) {
-            const int l = lane_id();
-            const unsigned long long mine = l < n ? D[l] : ~0ull;
-            const int rank = rank_of(D, n, mine);
-            __builtin_amdgcn_wave_barrier();
-            if (l < n) D[rank] = mine;
-        }
-        __syncthreads();
-    } else {
-        sort_keys(D, n);
-    }
+// Sort D[0..n) ascending (best first) in LDS with the whole block.
+__device__ __forceinline__ void sort_top(unsigned long long *D, int n, Misc &ms) {
+    sort_keys(D, n, ms.part);
 }
 
 // Kept prefix of D[0..n) (sorted best first, n <= 64) under top-p: the first entry whose
@@ -1637,7 +1656,7 @@ __device__ __forceinline__ int select_top(const unsigned long long *A, int n, in
         t = gather_keys(src, tau, D, cap, ms);
         if (t > cap) return -1;
     }
-    sort_top(D, t);
+    sort_top(D, t, ms);
     // keep the R best and the ties of the R-th
     const float tau = desc_key_y(D[R - 1]);
     int c = 0;
@@ -1770,7 +1789,6 @@ __device__ __forceinline__ void wave_rank_sort(unsigned long long *D, int t) {
 __device__ __forceinline__ bool topk_wave_tail(const Args &a, int row, int mode, const klsample_row_params &p,
                                                unsigned long long *A, int nF, unsigned long long *D, int t, int kk) {
     const int l = lane_id();
-    wave_rank_sort(D, t);
     const float xt = quotient_threshold(__fdiv_rn(desc_key_y(D[kk - 1]), p.temperature), p.temperature);
     unsigned long long *E = D + 256;
     int mine = 0;
@@ -1996,7 +2014,7 @@ __device__ __forceinline__ bool combine_row(const Args &a, int row, const klsamp
         if (R < nF) return select_top(A, nF, R, ylo, yhi, D, kSortCap, ms);
         for (int i = tid; i < nF; i += kThreads) D[i] = A[i];
         __syncthreads();
-        sort_top(D, nF);
+        sort_top(D, nF, ms);
         return nF;
     };
 
@@ -2073,7 +2091,8 @@ __device__ __forceinline__ bool combine_row(const Args &a, int row, const klsamp
         if (nF > kk && N <= 64) {
             // one histogram pass isolates the kk best, then one wave does the rest
             const int t = hist_gather(A, nF, kk, ylo, yhi, D, kSortCap, ms);
-            if (t >= 0 && t <= 256) {
+            if (t >= kk && t <= 256) {
+                block_rank_sort(D, t, ms.part);
                 if (wave_id() == 0) {
                     const bool done = topk_wave_tail(a, row, mode, p, A, nF, D, t, kk);
                     if (lane_id() == 0) ms.flag = done ? 1 : 0;
@@ -2094,7 +2113,7 @@ __device__ __forceinline__ bool combine_row(const Args &a, int row, const klsamp
             D[i] = desc_key(__fdiv_rn(desc_key_y(k), p.temperature), desc_key_idx(k));
         }
         __syncthreads();
-        sort_top(D, lk);
+        sort_top(D, lk, ms);
         const double mref = (double)desc_key_y(D[0]);
         const bool topp = (p.flags & KLSAMPLE_ROW_TOP_P) != 0;
         if (lk <= 64 && N <= 64) {
@@ -2126,8 +2145,8 @@ __device__ __forceinline__ bool combine_row(const Args &a, int row, const klsamp
     if (nF > 64 && N <= 64) {
         const int t = hist_gather(A, nF, 64, ylo, yhi, D, kSortCap, ms);
         if (t >= 0 && t <= 256) {
+            block_rank_sort(D, t, ms.part);
             if (wave_id() == 0) {
-                wave_rank_sort(D, t);
                 const int cut = wave_topp(D, min(t, 64), mref, Z, p.top_p);
                 if (cut > 0) wave_finish(a, row, mode, p, D, t, cut, mref, A);
                 if (lane_id() == 0) ms.flag = cut > 0 ? 1 : 0;
