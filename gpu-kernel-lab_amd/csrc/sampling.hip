@@ -134,6 +134,7 @@ struct Misc : Red {
     int ri[2][kWaves];
     uint32_t hist[256];
     uint32_t part[kThreads];   // block_rank_sort: per-thread partial ranks
+    uint32_t irank[64];        // block_index_rank: vocab-order ranks of a kept list
     unsigned long long hmass[256];
     int topn_idx[kMaxLogprobs];
     float topn_y[kMaxLogprobs];
@@ -147,6 +148,7 @@ struct Misc : Red {
     uint32_t sel_above_count;
     int sel_found;
     int ia, ib;
+    int ne;          // entries of a row's top set (top-k finish)
     uint32_t kmin, kmax;
     double da, db;
     TopPCut topp;
@@ -900,36 +902,6 @@ __device__ __forceinline__ float desc_key_y(unsigned long long k) { return fkey_
 __device__ __forceinline__ int desc_key_idx(unsigned long long k) { return (int)(uint32_t)k; }
 
 
-// Sort n <= kThreads distinct keys ascending in place: each thread ranks one key
-// against all n (LDS broadcast reads) and stores it at its rank.  Two barriers,
-// against ~log2(n)^2/2 for a bitonic network.
-__device__ __forceinline__ int rank_of(const unsigned long long *sb, int n, unsigned long long mine) {
-    // broadcast reads of two keys at a time; they do not depend on each other, so the
-    // loads pipeline (sb is 16-byte aligned; an odd n reads one key past the end, which
-    // is not counted)
-    int rank = 0;
-#pragma unroll 4
-    for (int j = 0; j < n; j += 2) {
-        const ulonglong2 q = *reinterpret_cast<const ulonglong2 *>(&sb[j]);
-        rank += (q.x < mine) ? 1 : 0;
-        rank += (j + 1 < n && q.y < mine) ? 1 : 0;
-    }
-    return rank;
-}
-
-__device__ __forceinline__ void rank_sort(unsigned long long *sb, int n) {
-    const int t = threadIdx.x;
-    unsigned long long mine = 0ull;
-    int rank = 0;
-    if (t < n) {
-        mine = sb[t];
-        rank = rank_of(sb, n, mine);
-    }
-    __syncthreads();
-    if (t < n) sb[rank] = mine;
-    __syncthreads();
-}
-
 // Sort sb[0..n) (distinct keys, 2 <= n <= kThreads) ascending with the whole block:
 // the kThreads / n threads given to a key each count the keys below it in one slice of
 // sb (broadcast 16-byte reads), and the slices' counts are added.  `part` holds
@@ -958,6 +930,33 @@ __device__ __forceinline__ void block_rank_sort(unsigned long long *sb, int n, u
         for (int g = 0; g < segs; ++g) rank += (int)part[g * n + tid];
     __syncthreads();
     if (tid < n) sb[rank] = key;
+    __syncthreads();
+}
+
+// Vocab-order ranks of the entries D[0..L) (1 <= L <= 64, distinct indices) into
+// irank[0..L), counted by the whole block as in block_rank_sort.  Two barriers.
+__device__ __forceinline__ void block_index_rank(const unsigned long long *D, int L, uint32_t *part, uint32_t *irank) {
+    const int tid = threadIdx.x;
+    const int segs = kThreads / L;
+    const int k = tid % L, sg = tid / L;
+    const int len = (((L + segs - 1) / segs) + 1) & ~1;
+    uint32_t cnt = 0u;
+    if (sg < segs) {
+        const int mine = desc_key_idx(D[k]);
+        const int j0 = sg * len, j1 = min(L, j0 + len);
+        for (int j = j0; j < j1; j += 2) {
+            const ulonglong2 q = *reinterpret_cast<const ulonglong2 *>(&D[j]);
+            cnt += (desc_key_idx(q.x) < mine) ? 1u : 0u;
+            cnt += (j + 1 < j1 && desc_key_idx(q.y) < mine) ? 1u : 0u;
+        }
+    }
+    part[tid] = cnt;
+    __syncthreads();
+    if (tid < L) {
+        uint32_t r = 0u;
+        for (int g = 0; g < segs; ++g) r += part[g * L + tid];
+        irank[tid] = r;
+    }
     __syncthreads();
 }
 
@@ -1538,7 +1537,7 @@ __device__ __forceinline__ void wave_write(const Args &a, int row, int mode, con
 // LDS reads), places their weights in index order and takes one prefix scan.
 __device__ __forceinline__ void wave_finish(const Args &a, int row, int mode, const klsample_row_params &p,
                                             const unsigned long long *D, int n, int L, double mref,
-                                            unsigned long long *scr) {
+                                            unsigned long long *scr, const uint32_t *irank = nullptr) {
     const int l = lane_id();
     const bool kept = l < L;
     const unsigned long long key = kept ? D[l] : ~0ull;
@@ -1546,11 +1545,15 @@ __device__ __forceinline__ void wave_finish(const Args &a, int row, int mode, co
     const int idx = kept ? desc_key_idx(key) : 0x7fffffff;
     const double w = kept ? (double)__expf(y - (float)mref) : 0.0;
     int rank = 0;
+    if (irank != nullptr) {
+        rank = kept ? (int)irank[l] : 0;
+    } else {
 #pragma unroll 4
-    for (int j = 0; j < L; j += 2) {
-        const ulonglong2 q = *reinterpret_cast<const ulonglong2 *>(&D[j]);
-        rank += (desc_key_idx(q.x) < idx) ? 1 : 0;
-        rank += (j + 1 < L && desc_key_idx(q.y) < idx) ? 1 : 0;
+        for (int j = 0; j < L; j += 2) {
+            const ulonglong2 q = *reinterpret_cast<const ulonglong2 *>(&D[j]);
+            rank += (desc_key_idx(q.x) < idx) ? 1 : 0;
+            rank += (j + 1 < L && desc_key_idx(q.y) < idx) ? 1 : 0;
+        }
     }
     const double zf = wave_reduce(w, OpSumD(), 0.0);
     RowOut r;
@@ -1731,93 +1734,6 @@ __device__ __forceinline__ int hist_gather(const unsigned long long *A, int n, i
     return ms.ib;
 }
 
-// Ranks of the keys a lane holds (J of them) among sb[0..n): one pass of broadcast
-// reads, two keys per read, compared with all J keys.
-template <int J>
-__device__ __forceinline__ void rank_of_multi(const unsigned long long *sb, int n, const unsigned long long (&mine)[J],
-                                              int (&rank)[J]) {
-#pragma unroll
-    for (int k = 0; k < J; ++k) rank[k] = 0;
-#pragma unroll 4
-    for (int j = 0; j < n; j += 2) {
-        const ulonglong2 q = *reinterpret_cast<const ulonglong2 *>(&sb[j]);
-        const bool second = j + 1 < n;
-#pragma unroll
-        for (int k = 0; k < J; ++k) {
-            rank[k] += (q.x < mine[k]) ? 1 : 0;
-            rank[k] += (second && q.y < mine[k]) ? 1 : 0;
-        }
-    }
-}
-
-// One wave: sort D[0..t) (t <= 256, distinct keys) ascending, up to four keys per lane.
-__device__ __forceinline__ void wave_rank_sort(unsigned long long *D, int t) {
-    const int l = lane_id();
-    if (t <= 64) {
-        const unsigned long long k1[1] = {l < t ? D[l] : ~0ull};
-        int r1[1];
-        rank_of_multi<1>(D, t, k1, r1);
-        __builtin_amdgcn_wave_barrier();
-        if (l < t) D[r1[0]] = k1[0];
-    } else if (t <= 128) {
-        const unsigned long long k2[2] = {D[l], l + 64 < t ? D[l + 64] : ~0ull};
-        int r2[2];
-        rank_of_multi<2>(D, t, k2, r2);
-        __builtin_amdgcn_wave_barrier();
-        D[r2[0]] = k2[0];
-        if (l + 64 < t) D[r2[1]] = k2[1];
-    } else {
-        unsigned long long k4[4];
-        int r4[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) k4[j] = l + 64 * j < t ? D[l + 64 * j] : ~0ull;
-        rank_of_multi<4>(D, t, k4, r4);
-        __builtin_amdgcn_wave_barrier();
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-            if (l + 64 * j < t) D[r4[j]] = k4[j];
-    }
-    __builtin_amdgcn_wave_barrier();
-}
-
-// One wave finishes a top-k row.  D[0..t) (t <= 256) holds the candidates of the
-// histogram bins at or above the kk-th one's, as scores before the division by T; A[0..nF)
-// holds every candidate.  Sorts D, takes the kk-th score's quotient, gathers every
-// candidate whose quotient reaches it (ties created by the division included), divides
-// and sorts them, applies top-p and writes the row.  Returns false, having written
-// nothing, when that top set exceeds 64 entries.
-__device__ __forceinline__ bool topk_wave_tail(const Args &a, int row, int mode, const klsample_row_params &p,
-                                               unsigned long long *A, int nF, unsigned long long *D, int t, int kk) {
-    const int l = lane_id();
-    const float xt = quotient_threshold(__fdiv_rn(desc_key_y(D[kk - 1]), p.temperature), p.temperature);
-    unsigned long long *E = D + 256;
-    int mine = 0;
-    for (int i = l; i < nF; i += 64) mine += (desc_key_y(A[i]) >= xt) ? 1 : 0;
-    const int incl = wave_incl_scan(mine);
-    const int lk = readlane(incl, 63);
-    if (lk > 64) return false;
-    int pos = incl - mine;
-    for (int i = l; i < nF; i += 64) {
-        const unsigned long long k = A[i];
-        const float x = desc_key_y(k);
-        if (x >= xt) E[pos++] = desc_key(__fdiv_rn(x, p.temperature), desc_key_idx(k));
-    }
-    __builtin_amdgcn_wave_barrier();
-    const unsigned long long mk = l < lk ? E[l] : ~0ull;
-    const int rank = rank_of(E, lk, mk);
-    __builtin_amdgcn_wave_barrier();
-    if (l < lk) E[rank] = mk;
-    __builtin_amdgcn_wave_barrier();
-    const double mref = (double)desc_key_y(E[0]);
-    int L = lk;
-    if (p.flags & KLSAMPLE_ROW_TOP_P) {
-        const double w = l < lk ? (double)__expf(desc_key_y(E[l]) - (float)mref) : 0.0;
-        const int cut = wave_topp(E, lk, mref, wave_reduce(w, OpSumD(), 0.0), p.top_p);
-        if (cut > 0) L = cut;
-    }
-    wave_finish(a, row, mode, p, E, lk, L, mref, A);
-    return true;
-}
 
 // Emit a row's outputs with its top-N list in D[0..count): one wave when the list is
 // short, else the block writer.
@@ -1898,7 +1814,7 @@ __device__ __forceinline__ bool combine_row(const Args &a, int row, const klsamp
         ms.rf[0][wave_id()] = m; ms.rf[1][wave_id()] = lo;
         ms.ri[0][wave_id()] = nfinite; ms.ri[1][wave_id()] = ovf;
     }
-    if (tid == 0) { ms.ncand = 0; ms.ia = 0x7fffffff; ms.ib = 0; ms.kmin = 0xffffffffu; ms.kmax = 0u; }
+    if (tid == 0) { ms.ncand = 0; ms.ia = 0x7fffffff; ms.ib = 0; ms.ne = 0; ms.kmin = 0xffffffffu; ms.kmax = 0u; }
     __syncthreads();
     m = ms.rf[0][0]; lo = ms.rf[1][0]; nfinite = ms.ri[0][0]; ovf = ms.ri[1][0];
 #pragma unroll
@@ -2089,16 +2005,42 @@ __device__ __forceinline__ bool combine_row(const Args &a, int row, const klsamp
         // divided and sorted in final space.
         const int kk = p.top_k;
         if (nF > kk && N <= 64) {
-            // one histogram pass isolates the kk best, then one wave does the rest
+            // one histogram pass isolates the kk best; sorted, they give the kk-th
+            // quotient, and the top set (every candidate whose quotient reaches it) is
+            // gathered, divided and sorted; one wave applies top-p and finishes
             const int t = hist_gather(A, nF, kk, ylo, yhi, D, kSortCap, ms);
             if (t >= kk && t <= 256) {
                 block_rank_sort(D, t, ms.part);
-                if (wave_id() == 0) {
-                    const bool done = topk_wave_tail(a, row, mode, p, A, nF, D, t, kk);
-                    if (lane_id() == 0) ms.flag = done ? 1 : 0;
+                const float xt = quotient_threshold(__fdiv_rn(desc_key_y(D[kk - 1]), p.temperature), p.temperature);
+                unsigned long long *Et = D + 256;
+                for (int i = tid; i < nF; i += kThreads) {
+                    const unsigned long long k = A[i];
+                    const float x = desc_key_y(k);
+                    if (x >= xt) {
+                        const int pos = wave_append(&ms.ne);
+                        if (pos < 64) Et[pos] = desc_key(__fdiv_rn(x, p.temperature), desc_key_idx(k));
+                    }
                 }
                 __syncthreads();
-                if (ms.flag) return true;
+                const int lk = ms.ne;
+                if (lk <= 64) {
+                    if (lk > 1) block_rank_sort(Et, lk, ms.part);
+                    const double mref = (double)desc_key_y(Et[0]);
+                    if (wave_id() == 0) {
+                        int L = lk;
+                        if (p.flags & KLSAMPLE_ROW_TOP_P) {
+                            const double w = lane_id() < lk ? (double)__expf(desc_key_y(Et[lane_id()]) - (float)mref) : 0.0;
+                            const int cut = wave_topp(Et, lk, mref, wave_reduce(w, OpSumD(), 0.0), p.top_p);
+                            if (cut > 0) L = cut;
+                        }
+                        if (lane_id() == 0) ms.flag = L;
+                    }
+                    __syncthreads();
+                    const int L = ms.flag;
+                    block_index_rank(Et, L, ms.part, ms.irank);
+                    if (wave_id() == 0) wave_finish(a, row, mode, p, Et, lk, L, mref, A, ms.irank);
+                    return true;
+                }
             }
         }
         float xt = kNegInf;
@@ -2148,11 +2090,15 @@ __device__ __forceinline__ bool combine_row(const Args &a, int row, const klsamp
             block_rank_sort(D, t, ms.part);
             if (wave_id() == 0) {
                 const int cut = wave_topp(D, min(t, 64), mref, Z, p.top_p);
-                if (cut > 0) wave_finish(a, row, mode, p, D, t, cut, mref, A);
-                if (lane_id() == 0) ms.flag = cut > 0 ? 1 : 0;
+                if (lane_id() == 0) ms.flag = cut;
             }
             __syncthreads();
-            if (ms.flag) return true;
+            const int cut = ms.flag;
+            if (cut > 0) {
+                block_index_rank(D, cut, ms.part, ms.irank);
+                if (wave_id() == 0) wave_finish(a, row, mode, p, D, t, cut, mref, A, ms.irank);
+                return true;
+            }
         }
     }
     int n = 0, L = -1;
