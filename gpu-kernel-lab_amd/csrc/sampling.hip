@@ -1688,15 +1688,19 @@ __device__ __forceinline__ float quotient_threshold(float y, float T) {
 
 // Block: the entries of A[0..n) (n > R >= 1) in the linear histogram bins (256 over
 // [ylo, yhi]) at or above the bin of the R-th largest, into D (capacity cap), unsorted.
-// ms.hist must be zero and ms.ib the zero counter.  Returns their count (D holds at
-// most cap of them), or -1 for a degenerate range.  Two barriers: every wave finds the
-// bin from the same histogram.
+// ms.hist must be zero unless ms_hist_dirty (then it is cleared first) and ms.ib the
+// zero counter.  Returns their count (D holds at most cap of them), or -1 for a
+// degenerate range.  Two barriers: every wave finds the bin from the same histogram.
 __device__ __forceinline__ int hist_gather(const unsigned long long *A, int n, int R, float ylo, float yhi,
-                                           unsigned long long *D, int cap, Misc &ms) {
+                                           unsigned long long *D, int cap, Misc &ms, bool ms_hist_dirty) {
     const float span = yhi - ylo;
     const float scale = 256.f / span;
     if (!(span > 0.f) || !(scale <= __FLT_MAX__)) return -1;
     auto bin = [&](unsigned long long k) { return min(255, (int)((desc_key_y(k) - ylo) * scale)); };
+    if (ms_hist_dirty) {
+        for (int i = threadIdx.x; i < 256; i += kThreads) ms.hist[i] = 0u;
+        __syncthreads();
+    }
     for (int i = threadIdx.x; i < n; i += kThreads) atomicAdd(&ms.hist[bin(A[i])], 1u);
     __syncthreads();
     const int l = lane_id();
@@ -1915,6 +1919,7 @@ __device__ __forceinline__ bool combine_row(const Args &a, int row, const klsamp
     arg = ms.ia;
     int nF = ms.ncand;
     float ylo = fkey_inv(ms.kmin), yhi = fkey_inv(ms.kmax);
+    const bool narrowed = nF > kSortCap;   // the radix narrowing below leaves ms.hist used
     if (nF > kSortCap) {
         // too many candidates for LDS: narrow them to the best R with a radix select over
         // the candidate slots
@@ -2008,7 +2013,7 @@ __device__ __forceinline__ bool combine_row(const Args &a, int row, const klsamp
             // one histogram pass isolates the kk best; sorted, they give the kk-th
             // quotient, and the top set (every candidate whose quotient reaches it) is
             // gathered, divided and sorted; one wave applies top-p and finishes
-            const int t = hist_gather(A, nF, kk, ylo, yhi, D, kSortCap, ms);
+            const int t = hist_gather(A, nF, kk, ylo, yhi, D, kSortCap, ms, narrowed);
             if (t >= kk && t <= 256) {
                 block_rank_sort(D, t, ms.part);
                 const float xt = quotient_threshold(__fdiv_rn(desc_key_y(D[kk - 1]), p.temperature), p.temperature);
@@ -2085,7 +2090,7 @@ __device__ __forceinline__ bool combine_row(const Args &a, int row, const klsamp
     // top-p alone: the best 64 (one wave), then the best 256, then every candidate
     const double mref = (double)m;
     if (nF > 64 && N <= 64) {
-        const int t = hist_gather(A, nF, 64, ylo, yhi, D, kSortCap, ms);
+        const int t = hist_gather(A, nF, 64, ylo, yhi, D, kSortCap, ms, narrowed);
         if (t >= 0 && t <= 256) {
             block_rank_sort(D, t, ms.part);
             if (wave_id() == 0) {

@@ -182,6 +182,25 @@ def test_long_histories_count_past_16_bits(dtype):
     check(out, rows, params, probs=True)
 
 
+@pytest.mark.parametrize('n', [0, 5])
+def test_wide_vocab_top_p_rows_narrow_their_candidates(n):
+    """Top-p rows over 74 chunks gather more candidates than the row's LDS list holds;
+    the combine narrows them with a radix select before the histogram gather."""
+    say(f'wide vocab top-p n={n}')
+    rng = np.random.default_rng(13)
+    V = 600001
+    x = (rng.standard_normal((6, V)) * 2).astype(np.float32)
+    x[1, rng.choice(V, 300, replace=False)] += 9.0          # heavy head
+    x[3, rng.choice(V, 40, replace=False)] += 14.0
+    logits = torch.from_numpy(x)
+    params = [SamplingParams(temperature=t, top_p=tp, logprobs=n)
+              for t, tp in ((0.8, 0.9), (0.7, 0.95), (1.0, 0.5), (0.9, 0.99), (1.3, 0.3), (0.6, 0.8))]
+    u = rng.random(6).astype(np.float32)
+    rows = sample_rows(logits, None, params, u)
+    out = run(logits, params, None, u, probs=True)
+    check(out, rows, params, probs=True)
+
+
 def test_massive_ties_take_the_row_path():
     say('ties: constant rows')
     V = 50000
