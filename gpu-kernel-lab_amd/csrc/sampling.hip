@@ -360,8 +360,9 @@ __device__ __forceinline__ float element_final(const Args &a, const klsample_row
 // wave has Kw elements at or above it, K in all.  The waves search in parallel, by
 // bisection over order-preserving keys with ballots, without barriers.
 
-// Kw-th largest group-maximum key of the calling wave (low 8 key bits zero, so it may
-// sit up to 2^-15 relative below the exact value).  Wave-uniform.
+// Kw-th largest group-maximum key of the calling wave (low 16 key bits zero, so it may
+// sit up to 2^-7 relative below the exact value: a few more candidates, eight fewer
+// bisection steps).  Wave-uniform.
 template <int E, int G>
 __device__ __forceinline__ uint32_t wave_group_bound(const float (&x)[E], int Kw) {
     constexpr int GS = E / G;
@@ -374,7 +375,7 @@ __device__ __forceinline__ uint32_t wave_group_bound(const float (&x)[E], int Kw
         k[g] = fkey(mx);
     }
     uint32_t t = 0u;
-    for (int bit = 31; bit >= 8; --bit) {
+    for (int bit = 31; bit >= 16; --bit) {
         const uint32_t cand = t | (1u << bit);
         int c = 0;
 #pragma unroll
@@ -2167,9 +2168,10 @@ struct ScanLds {
     static constexpr int value = penalty > keys ? penalty : keys;
 };
 
-// Streaming pass: one workgroup per (row, chunk).  The LDS footprint (at most ~19 KB)
-// lets eight workgroups share a CU; the register budget is capped so that five
-// (32 elements per thread) or eight waves per SIMD fit, to hide HBM latency.
+// Streaming pass: one workgroup per (row, chunk).  The LDS footprint (~26 KB at 32
+// elements per thread) lets six workgroups share a CU, and the register budget is
+// capped to match (80 VGPRs: six waves per SIMD; seven or eight for smaller chunks),
+// to hide HBM latency.
 //
 // Penalties: the row's history ids are counted into an LDS table and mark their
 // element in its owner's slot mask (atomics whose results nobody waits for).  A lane
@@ -2177,8 +2179,8 @@ struct ScanLds {
 // penalises the marked ones there (one per set mask bit) and reloads them, so the
 // dense work that follows (bound, candidates, sums) sees final scores everywhere
 // with no per-element branch.
-template <typename TIn, int E>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(E >= 32 ? 4 : E >= 16 ? 7 : 8))) void scan_kernel(Args a) {
+template <typename TIn, int E, bool kVec>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(E >= 32 ? 6 : E >= 16 ? 7 : 8))) void scan_kernel(Args a) {
     constexpr int VW = Loader<TIn>::VW;
     constexpr int NV = E / VW;
     constexpr int C = kThreads * E;
@@ -2226,30 +2228,23 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(E >= 3
         clear();
     }
 
+    // Rows that cannot take 16-byte loads (unaligned, or a last chunk shorter than one
+    // vector) run the kVec = false instantiation.  Otherwise every chunk takes the same
+    // vector loads, with addresses clamped to the last whole vector of a partial chunk
+    // (a no-op for full ones): one load path, so the history count below waits for the
+    // ids only, with the logits still in flight.  Positions past cn are masked after the
+    // count; the vector straddling cn (if any) is re-read element by element (every
+    // thread of a partial chunk reads it, its owner keeps it).
     float x[E];
-    if (cn == C && a.vec_ok) {
-        // full chunk: every 16-byte load issued back to back
-#pragma unroll
-        for (int v = 0; v < NV; ++v) Loader<TIn>::vec(src + (v * kThreads + tid) * VW, &x[v * VW]);
-    } else if (a.vec_ok && cn >= VW) {
-        // partial chunk: the same loads with addresses clamped to the last whole vector
-        // (never predicated, so they stay in flight together), positions past cn
-        // masked; the one vector straddling cn is re-read element by element
+    float ptail[VW];
+    if (kVec) {
         const int lastfull = (cn / VW - 1) * VW;
 #pragma unroll
         for (int v = 0; v < NV; ++v) Loader<TIn>::vec(src + min((v * kThreads + tid) * VW, lastfull), &x[v * VW]);
+        if (cn < C) {
+            const int ls = (cn / VW) * VW;
 #pragma unroll
-        for (int v = 0; v < NV; ++v) {
-            const int li = (v * kThreads + tid) * VW;
-#pragma unroll
-            for (int e = 0; e < VW; ++e) x[v * VW + e] = (li + e < cn) ? x[v * VW + e] : kNegInf;
-            if (li < cn && li + VW > cn) {
-#pragma unroll
-                for (int e = 0; e < VW; ++e) {
-                    const float t = Loader<TIn>::one(src + min(li + e, cn - 1));
-                    x[v * VW + e] = (li + e < cn) ? t : kNegInf;
-                }
-            }
+            for (int e = 0; e < VW; ++e) ptail[e] = Loader<TIn>::one(src + min(ls + e, cn - 1));
         }
     } else {
 #pragma unroll
@@ -2261,6 +2256,20 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(E >= 3
             }
         }
     }
+
+    auto mask_partial = [&]() {
+        if (kVec && cn < C) {
+            const int ls = (cn / VW) * VW;
+#pragma unroll
+            for (int v = 0; v < NV; ++v) {
+                const int li = (v * kThreads + tid) * VW;
+#pragma unroll
+                for (int e = 0; e < VW; ++e)
+                    x[v * VW + e] = (li + e < cn) ? (li >= ls ? ptail[e] : x[v * VW + e]) : kNegInf;
+            }
+        }
+    };
+    if (H == 0) mask_partial();
 
     if (H > 0) {
         // Counts the history ids falling in [lo, lo + span) of the chunk and marks their
@@ -2326,19 +2335,23 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(E >= 3
                 pend &= ~__ballot(mine);
             }
         };
-        // 32-bit counts of half a chunk fill the table: two parts
+        // 32-bit counts of half a chunk fill the table: two parts.  The first count
+        // stays outside the loop, so that it waits for the history ids only, not for
+        // the logits loaded after them.
         constexpr unsigned kHalf = C / 2;
         const int parts = packed ? 1 : 2;
         __syncthreads();   // table cleared
+        if (packed) count_part(std::false_type{}, 0u, (unsigned)C, true);
+        else count_part(std::true_type{}, 0u, kHalf, true);
+        mask_partial();
 #pragma unroll 1
         for (int part = 0; part < parts; ++part) {
             if (part > 0) {
                 __syncthreads();
                 clear();
                 __syncthreads();
+                count_part(std::true_type{}, kHalf, kHalf, false);
             }
-            if (packed) count_part(std::false_type{}, 0u, (unsigned)C, true);
-            else count_part(std::true_type{}, part * kHalf, kHalf, part == 0);
             __syncthreads();
             apply(!packed, part * kHalf);
         }
@@ -2533,7 +2546,10 @@ hipError_t launch_typed(const Args &a, hipStream_t s, const PhaseEvents *ph) {
     const dim3 grid((unsigned)((int64_t)a.B * a.S));
     hipError_t e = mark(ph, 0, s);
     if (e != hipSuccess) return e;
-    scan_kernel<TIn, E><<<grid, kThreads, 0, s>>>(a);
+    // 16-byte loads need aligned rows and a last chunk of at least one vector
+    const int tail = a.V - (a.S - 1) * a.C;
+    if (a.vec_ok && tail * (int)sizeof(TIn) >= 16) scan_kernel<TIn, E, true><<<grid, kThreads, 0, s>>>(a);
+    else scan_kernel<TIn, E, false><<<grid, kThreads, 0, s>>>(a);
     if ((e = mark(ph, 1, s)) != hipSuccess) return e;
     row_kernel<TIn, E><<<dim3((unsigned)a.B), kThreads, 0, s>>>(a);
     if ((e = mark(ph, 2, s)) != hipSuccess) return e;
