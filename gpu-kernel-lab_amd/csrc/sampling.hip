@@ -1702,7 +1702,20 @@ __device__ __forceinline__ int hist_gather(const unsigned long long *A, int n, i
         for (int i = threadIdx.x; i < 256; i += kThreads) ms.hist[i] = 0u;
         __syncthreads();
     }
-    for (int i = threadIdx.x; i < n; i += kThreads) atomicAdd(&ms.hist[bin(A[i])], 1u);
+    // each thread's entries (n <= kSortCap: at most kPer) and their bins stay in
+    // registers between the two passes
+    constexpr int kPer = kSortCap / kThreads;
+    unsigned long long key[kPer];
+    int bn[kPer];
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+        const int i = threadIdx.x + j * kThreads;
+        key[j] = A[min(i, n - 1)];
+        bn[j] = (i < n) ? bin(key[j]) : -1;
+    }
+#pragma unroll
+    for (int j = 0; j < kPer; ++j)
+        if (bn[j] >= 0) atomicAdd(&ms.hist[bn[j]], 1u);
     __syncthreads();
     const int l = lane_id();
     uint32_t c[4], sum = 0u;
@@ -1723,15 +1736,16 @@ __device__ __forceinline__ int hist_gather(const unsigned long long *A, int n, i
     }
     b = __builtin_amdgcn_readlane(b, fl);
     int mine = 0;
-    for (int i = threadIdx.x; i < n; i += kThreads) mine += (bin(A[i]) >= b) ? 1 : 0;
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) mine += (bn[j] >= b) ? 1 : 0;
     const int pincl = wave_incl_scan(mine);
     int base = 0;
     if (l == 63 && pincl > 0) base = atomicAdd(&ms.ib, pincl);
     base = readlane(base, 63) + pincl - mine;
-    for (int i = threadIdx.x; i < n; i += kThreads) {
-        const unsigned long long k = A[i];
-        if (bin(k) >= b) {
-            if (base < cap) D[base] = k;
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) {
+        if (bn[j] >= b) {
+            if (base < cap) D[base] = key[j];
             ++base;
         }
     }
