@@ -1877,8 +1877,12 @@ __device__ __forceinline__ bool combine_row(const Args &a, int row, const klsamp
         // the requested slots: accepted ones counted first, one LDS atomic per wave
         // reserves their places, then they are written
         uint32_t acc = 0u;
+        // slot rounds whose first chunk is past the requested ones are skipped by the
+        // whole wave
+        const int wq0 = __builtin_amdgcn_readfirstlane(wave_id() * 64);
 #pragma unroll
         for (int i = 0; i < kSpecLoads; ++i) {
+            if (((wq0 + i * kThreads) >> pshift) >= nspec) break;
             const int q = tid + i * kThreads;
             const int c = q >> pshift;
             const int nc0 = cnt[min(c, kMaxChunksLds - 1)];   // read unconditionally
@@ -1893,6 +1897,7 @@ __device__ __forceinline__ bool combine_row(const Args &a, int row, const klsamp
         base = readlane(base, 63) + incl - mine;
 #pragma unroll
         for (int i = 0; i < kSpecLoads; ++i) {
+            if (((wq0 + i * kThreads) >> pshift) >= nspec) break;
             if (acc & (1u << (2 * i))) {
                 if (base < kSortCap) A[base] = desc_key(__uint_as_float(spec[i].x), (int)spec[i].y);
                 ++base;
