@@ -961,6 +961,39 @@ __device__ __forceinline__ void block_index_rank(const unsigned long long *D, in
     __syncthreads();
 }
 
+// Sorts in[0..n) (2 <= n <= 64, distinct keys and indices) ascending into out, and
+// records at each sorted position the entry's rank in vocab order among all n
+// (irank).  Value and index comparisons share one pass of the whole block (the two
+// counts packed in one word); two barriers.
+__device__ __forceinline__ void block_rank_sort_idx(const unsigned long long *in, int n, unsigned long long *out,
+                                                    uint32_t *part, uint32_t *irank) {
+    const int tid = threadIdx.x;
+    const int segs = kThreads / n;
+    const int k = tid % n, sg = tid / n;
+    const int len = (((n + segs - 1) / segs) + 1) & ~1;
+    unsigned long long key = ~0ull;
+    uint32_t cnt = 0u;
+    if (sg < segs) {
+        key = in[k];
+        const int mine = desc_key_idx(key);
+        const int j0 = sg * len, j1 = min(n, j0 + len);
+        for (int j = j0; j < j1; j += 2) {
+            const ulonglong2 q = *reinterpret_cast<const ulonglong2 *>(&in[j]);
+            cnt += ((q.x < key) ? 1u : 0u) + ((desc_key_idx(q.x) < mine) ? 65536u : 0u);
+            if (j + 1 < j1) cnt += ((q.y < key) ? 1u : 0u) + ((desc_key_idx(q.y) < mine) ? 65536u : 0u);
+        }
+    }
+    part[tid] = cnt;
+    __syncthreads();
+    if (tid < n) {
+        uint32_t r = 0u;
+        for (int g = 0; g < segs; ++g) r += part[g * n + tid];
+        out[r & 0xffffu] = key;
+        irank[r & 0xffffu] = r >> 16;
+    }
+    __syncthreads();
+}
+
 // Sort n distinct keys ascending in LDS (capacity >= pow2_ceil(n)).
 __device__ __forceinline__ void sort_keys(unsigned long long *sb, int n, uint32_t *part) {
     if (n <= 1) return;
@@ -1538,16 +1571,20 @@ __device__ __forceinline__ void wave_write(const Args &a, int row, int mode, con
 // LDS reads), places their weights in index order and takes one prefix scan.
 __device__ __forceinline__ void wave_finish(const Args &a, int row, int mode, const klsample_row_params &p,
                                             const unsigned long long *D, int n, int L, double mref,
-                                            unsigned long long *scr, const uint32_t *irank = nullptr) {
+                                            unsigned long long *scr, const uint32_t *irank = nullptr,
+                                            bool ranked_all = false) {
     const int l = lane_id();
     const bool kept = l < L;
-    const unsigned long long key = kept ? D[l] : ~0ull;
-    const float y = kept ? desc_key_y(key) : kNegInf;
-    const int idx = kept ? desc_key_idx(key) : 0x7fffffff;
+    // ranked_all: irank holds vocab-order ranks among all n <= 64 entries; the entries
+    // past the kept prefix then take part in the ordered draw with weight 0
+    const bool placed = ranked_all ? (l < n) : kept;
+    const unsigned long long key = placed ? D[l] : ~0ull;
+    const float y = placed ? desc_key_y(key) : kNegInf;
+    const int idx = placed ? desc_key_idx(key) : 0x7fffffff;
     const double w = kept ? (double)__expf(y - (float)mref) : 0.0;
     int rank = 0;
     if (irank != nullptr) {
-        rank = kept ? (int)irank[l] : 0;
+        rank = placed ? (int)irank[l] : 0;
     } else {
 #pragma unroll 4
         for (int j = 0; j < L; j += 2) {
@@ -1565,22 +1602,25 @@ __device__ __forceinline__ void wave_finish(const Args &a, int row, int mode, co
     r.kept = L;
     r.log_norm = log(zf);
     __builtin_amdgcn_wave_barrier();
-    if (kept) {
+    if (placed) {
         scr[rank] = __double_as_longlong(w);
-        scr[64 + rank] = (unsigned long long)(uint32_t)idx;
+        scr[64 + rank] = (unsigned long long)(uint32_t)idx | (kept ? (1ull << 32) : 0ull);
     }
     __builtin_amdgcn_wave_barrier();
-    // lane i now holds the i-th smallest kept index: inverse CDF in vocab order
-    const double wi = kept ? __longlong_as_double(scr[l]) : 0.0;
-    const int ii = kept ? (int)(uint32_t)scr[64 + l] : 0;
+    // lane i now holds the i-th smallest placed index: inverse CDF in vocab order
+    const bool at_placed = ranked_all ? (l < n) : kept;
+    const unsigned long long sv = at_placed ? scr[64 + l] : 0ull;
+    const bool kf = (sv >> 32) != 0ull;
+    const double wi = at_placed ? __longlong_as_double(scr[l]) : 0.0;
+    const int ii = (int)(uint32_t)sv;
     const double cum = wave_incl_scan(wi);
     const double target = (double)p.uniform * zf;
-    const unsigned long long over = __ballot(kept && cum > target);
+    const unsigned long long over = __ballot(kf && cum > target);
     int lt;
     if (over) {
         lt = __ffsll((long long)over) - 1;
     } else {
-        const unsigned long long pos = __ballot(kept && wi > 0.0);
+        const unsigned long long pos = __ballot(kf && wi > 0.0);
         lt = pos ? 63 - __clzll((long long)pos) : 0;
     }
     r.token = __builtin_amdgcn_readlane(ii, lt);
@@ -2049,21 +2089,26 @@ __device__ __forceinline__ bool combine_row(const Args &a, int row, const klsamp
                 __syncthreads();
                 const int lk = ms.ne;
                 if (lk <= 64) {
-                    if (lk > 1) block_rank_sort(Et, lk, ms.part);
-                    const double mref = (double)desc_key_y(Et[0]);
+                    // sorted (into D + 128) with every entry's vocab-order rank; one wave
+                    // applies top-p and finishes
+                    unsigned long long *Es = Et;
+                    if (lk > 1) {
+                        Es = D + 128;
+                        block_rank_sort_idx(Et, lk, Es, ms.part, ms.irank);
+                    } else if (tid == 0) {
+                        ms.irank[0] = 0u;
+                    }
+                    if (lk <= 1) __syncthreads();
                     if (wave_id() == 0) {
+                        const double mref = (double)desc_key_y(Es[0]);
                         int L = lk;
                         if (p.flags & KLSAMPLE_ROW_TOP_P) {
-                            const double w = lane_id() < lk ? (double)__expf(desc_key_y(Et[lane_id()]) - (float)mref) : 0.0;
-                            const int cut = wave_topp(Et, lk, mref, wave_reduce(w, OpSumD(), 0.0), p.top_p);
+                            const double w = lane_id() < lk ? (double)__expf(desc_key_y(Es[lane_id()]) - (float)mref) : 0.0;
+                            const int cut = wave_topp(Es, lk, mref, wave_reduce(w, OpSumD(), 0.0), p.top_p);
                             if (cut > 0) L = cut;
                         }
-                        if (lane_id() == 0) ms.flag = L;
+                        wave_finish(a, row, mode, p, Es, lk, L, mref, A, ms.irank, true);
                     }
-                    __syncthreads();
-                    const int L = ms.flag;
-                    block_index_rank(Et, L, ms.part, ms.irank);
-                    if (wave_id() == 0) wave_finish(a, row, mode, p, Et, lk, L, mref, A, ms.irank);
                     return true;
                 }
             }
