@@ -233,6 +233,40 @@ def sampler_call_us(device, calls=200):
     return (time.perf_counter() - t0) * 1e6 / calls
 
 
+# the other configurations of the sampling path, each timed at its own shape (device time
+# per call, inputs resident): workload name, timed calls, warm-up calls
+OTHER_CONFIGS = (
+    ('cpu_reference_b8', 300, 30),
+    ('mixed_b64', 60, 6),
+    ('throughput_b256_v128256', 300, 30),
+    ('tie_stress_b1024', 60, 6),
+)
+
+
+def per_config(device):
+    """Device µs per call, rows/s and algorithmic GB/s of each other configuration."""
+    out = {}
+    for name, steps, warmup in OTHER_CONFIGS:
+        r = Resident(name, device)
+        _, d = timed_steps(r, steps, warmup)
+        out[name] = {'batch': r.w.batch, 'vocab': r.w.vocab, 'logits': str(r.w.logits.dtype).replace('torch.', ''),
+                     'device_us_per_call': round(d * 1e3, 2), 'rows_per_s': round(r.w.batch / (d * 1e-3), 1),
+                     'alg_gbs': round(r.alg_bytes / (d * 1e-3) / 1e9, 1)}
+        del r
+    return out
+
+
+def cpu_model():
+    try:
+        with open('/proc/cpuinfo') as f:
+            for line in f:
+                if line.startswith('model name'):
+                    return line.split(':', 1)[1].strip()
+    except OSError:
+        pass
+    return 'unknown'
+
+
 def cpu_baseline(seconds):
     """The oracle's faithful mode (torch CPU ops of serving/sampling.py:44-63 including
     torch.multinomial), one call per row of the headline batch, until ``seconds`` pass."""
@@ -250,12 +284,26 @@ def cpu_baseline(seconds):
         restated_sample(w.logits[b], w.histories[b], w.params[b], generator=gens[b], diagnostics=False)
         n += 1
     el = time.perf_counter() - t0
+    # the same on one thread, for a quarter of the time
+    torch.set_num_threads(1)
+    n1 = 0
+    t1 = time.perf_counter()
+    while time.perf_counter() - t1 < seconds / 4:
+        b = n1 % w.batch
+        restated_sample(w.logits[b], w.histories[b], w.params[b], generator=gens[b], diagnostics=False)
+        n1 += 1
+    el1 = time.perf_counter() - t1
+    torch.set_num_threads(threads)
     return {
         'value': round(n / el, 3), 'unit': 'rows/s', 'cores': threads, 'kind': 'port',
         'sample': (f'{n} row calls cycling over the B=256, V=151936 fp32 batch (T=1, top_k=40, top_p=0.9, '
                    f'three penalties, 2048-id histories), one restated Sampler.sample call per row with '
                    f'torch.multinomial, {threads} torch CPU threads, {el:.1f} s; {el / n * 1e3:.2f} ms/row; '
                    f'torch {torch.__version__}'),
+        'cpu_model': cpu_model(),
+        'host_cpus': os.cpu_count(),
+        'one_thread': {'value': round(n1 / el1, 3), 'unit': 'rows/s',
+                       'sample': f'{n1} row calls, 1 torch CPU thread, {el1:.1f} s; {el1 / n1 * 1e3:.2f} ms/row'},
     }
 
 
@@ -425,6 +473,7 @@ def main():
         lat[key] = round(d * 1e3, 2)
         del r1
     lat['sampler_call_wall'] = round(sampler_call_us(device), 1)
+    configs = per_config(device)
 
     achieved = res.alg_bytes / (scan_ms * 1e-3) / 1e9
     out = {
@@ -448,6 +497,7 @@ def main():
         'device_us_per_step': round(dev_ms * 1e3, 2),
         'kernels_us': {'scan_kernel': round(scan_ms * 1e3, 2), 'row_kernel': round(comb_ms * 1e3, 2)},
         'b1_latency_us': lat,
+        'other_configs': configs,
         'roofline': {'bound': 'hbm', 'achieved': round(achieved, 1), 'peak': PEAK_HBM_GBS, 'unit': 'GB/s',
                      'frac': round(achieved / PEAK_HBM_GBS, 4), 'traffic': read_traffic()},
         'outputs_consistent': consistent,
