@@ -549,24 +549,33 @@ struct DenseSource {
     int cut_idx;
     __device__ __forceinline__ bool keep(float v, int i) const { return v > cut || (v == cut && i <= cut_idx); }
     // Calls f(key, index, score) for every kept entry.  y is 16-byte aligned and
-    // readable up to V rounded up to 4: eight 16-byte loads are in flight per thread.
+    // readable up to V rounded up to 4.  Blocks of eight 16-byte loads per thread: the
+    // next block is requested before the current one is visited (addresses clamped, so
+    // the request past the end is a harmless re-read), sixteen loads in flight.
     template <class F>
     __device__ __forceinline__ void each(F f) const {
         constexpr int U = 8;
+        constexpr int kStep = kThreads * 4 * U;
         const int vlast = (V - 1) & ~3;
-        for (int t0 = 0; t0 < V; t0 += kThreads * 4 * U) {
-            float4 q[U];
+        float4 qa[U], qb[U];
+        auto request = [&](float4 (&q)[U], int t0) {
 #pragma unroll
             for (int u = 0; u < U; ++u)
                 q[u] = *reinterpret_cast<const float4 *>(y + min(t0 + (u * kThreads + (int)threadIdx.x) * 4, vlast));
+        };
+        request(qa, 0);
+        for (int t0 = 0; t0 < V; t0 += kStep) {
+            request(qb, t0 + kStep);
 #pragma unroll
             for (int u = 0; u < U; ++u) {
                 const int i = t0 + (u * kThreads + (int)threadIdx.x) * 4;
-                const float v4[4] = {q[u].x, q[u].y, q[u].z, q[u].w};
+                const float v4[4] = {qa[u].x, qa[u].y, qa[u].z, qa[u].w};
 #pragma unroll
                 for (int e = 0; e < 4; ++e)
                     if (i + e < V && keep(v4[e], i + e)) f(fkey(v4[e]), i + e, v4[e]);
             }
+#pragma unroll
+            for (int u = 0; u < U; ++u) qa[u] = qb[u];
         }
     }
 };
@@ -853,6 +862,130 @@ __device__ __forceinline__ int ordered_find(int n, W weight, double target, Misc
     __syncthreads();
     const int found = ms.ib;
     before = ms.db;
+    __syncthreads();
+    return found;
+}
+
+// Inverse CDF over a dense source in vocab order: the first kept entry whose inclusive
+// cumulative weight_fix(y, m) exceeds `target` (same fixed point), or -1; `last`
+// receives the last kept entry of positive weight (-1 if none).  Segments of
+// kDrawStep * g consecutive entries (at most kSegCap of them), one wave per segment:
+// segment sums from 16-byte loads, the wave's next step requested before the current
+// one is summed; then wave 0 finds the crossing segment and walks it.  The sums are
+// integers, exact and independent of their order, so the crossing segment holds the
+// crossing entry.
+constexpr int kDrawStep = 64 * 4 * 8;   // entries per wave step: eight 16-byte loads per lane
+
+__device__ __forceinline__ int dense_draw(const DenseSource &src, float m, unsigned long long target, Misc &ms,
+                                          int &last) {
+    const int V = src.V;
+    int g = 1;
+    while ((V + kDrawStep * g - 1) / (kDrawStep * g) > kSegCap) g <<= 1;
+    const int seg = kDrawStep * g;
+    const int nseg = (V + seg - 1) / seg;
+    const int lane = lane_id(), w = wave_id();
+    const int vlast = (V - 1) & ~3;
+    unsigned long long *segq = reinterpret_cast<unsigned long long *>(ms.seg);
+    auto request = [&](float4 (&q)[8], int base) {
+#pragma unroll
+        for (int u = 0; u < 8; ++u) q[u] = *reinterpret_cast<const float4 *>(src.y + min(base + (u * 64 + lane) * 4, vlast));
+    };
+    auto weight = [&](float v, int i) -> unsigned long long {
+        return (i < V && src.keep(v, i)) ? weight_fix(v, m) : 0ull;
+    };
+    // 1. segment sums: wave w takes segments w, w + kWaves, ... step by step
+    const int nsteps = ((nseg - w + kWaves - 1) / kWaves) * g;
+    auto step_base = [&](int k) { return (w + kWaves * (k / g)) * seg + (k % g) * kDrawStep; };
+    float4 qa[8], qb[8];
+    request(qa, step_base(0));
+    unsigned long long sum = 0ull;
+    int lp = -1;
+    for (int k = 0; k < nsteps; ++k) {
+        request(qb, step_base(min(k + 1, nsteps - 1)));
+        const int b = step_base(k);
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int i0 = b + (u * 64 + lane) * 4;
+            const float v4[4] = {qa[u].x, qa[u].y, qa[u].z, qa[u].w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const unsigned long long wt = weight(v4[e], i0 + e);
+                sum += wt;
+                if (wt) lp = i0 + e;
+            }
+        }
+        if (k % g == g - 1) {
+            sum = wave_reduce(sum, OpSumQ(), 0ull);
+            lp = wave_reduce(lp, OpMaxI(), -1);
+            if (lane == 0) { segq[w + kWaves * (k / g)] = sum; ms.segl[w + kWaves * (k / g)] = lp; }
+            sum = 0ull;
+            lp = -1;
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) qa[u] = qb[u];
+    }
+    __syncthreads();
+    // 2. the crossing segment (two per lane)
+    if (w == 0) {
+        const int s0 = 2 * lane, s1 = 2 * lane + 1;
+        const unsigned long long a0 = s0 < nseg ? segq[s0] : 0ull, a1 = s1 < nseg ? segq[s1] : 0ull;
+        const int l2 = max(s0 < nseg ? ms.segl[s0] : -1, s1 < nseg ? ms.segl[s1] : -1);
+        const unsigned long long incl = wave_incl_scan(a0 + a1);
+        const unsigned long long ex = incl - (a0 + a1);
+        const bool c0 = s0 < nseg && ex + a0 > target;
+        const bool c1 = s1 < nseg && ex + a0 + a1 > target;
+        const unsigned long long bal = __ballot(c0 || c1);
+        const int lpm = wave_reduce(l2, OpMaxI(), -1);
+        if (bal == 0ull) {
+            if (lane == 0) ms.ia = -1;
+        } else if (lane == __ffsll((long long)bal) - 1) {
+            ms.ia = c0 ? s0 : s1;
+            ms.sel_above_mass = c0 ? ex : ex + a0;
+        }
+        if (lane == 0) ms.last = lpm;
+    }
+    __syncthreads();
+    const int sg = ms.ia;
+    last = ms.last;
+    // 3. its walk, one step (eight loads per lane) at a time
+    if (w == 0 && sg >= 0) {
+        unsigned long long run = ms.sel_above_mass;
+        int found = -1;
+        for (int k = 0; k < g && found < 0; ++k) {
+            const int b = sg * seg + k * kDrawStep;
+            request(qa, b);
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                if (found >= 0) break;
+                const int i0 = b + (u * 64 + lane) * 4;
+                const float v4[4] = {qa[u].x, qa[u].y, qa[u].z, qa[u].w};
+                unsigned long long wv[4], ls = 0ull;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) { wv[e] = weight(v4[e], i0 + e); ls += wv[e]; }
+                const unsigned long long incl = run + wave_incl_scan(ls);
+                const unsigned long long bal = __ballot(incl > target);
+                if (bal != 0ull) {
+                    const int fl = __ffsll((long long)bal) - 1;
+                    int f = -1;
+                    if (lane == fl) {
+                        unsigned long long c = incl - ls;
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            if (f < 0 && c + wv[e] > target) f = i0 + e;
+                            c += wv[e];
+                        }
+                    }
+                    found = readlane(f, fl);
+                } else {
+                    run = readlane(incl, 63);
+                }
+            }
+        }
+        if (found < 0) found = ms.segl[sg];
+        if (lane == 0) ms.ib = found;
+    }
+    __syncthreads();
+    const int found = sg >= 0 ? ms.ib : -1;
     __syncthreads();
     return found;
 }
@@ -1278,39 +1411,81 @@ __device__ __forceinline__ int topp_cut_bins(const DenseSource &src, float m, fl
 // candidates cannot settle the row.
 template <typename TIn, int E>
 __device__ __forceinline__ void dense_resolve(const Args &a, int row, const klsample_row_params &p, int mode,
-                              unsigned char *raw, Misc &ms) {
+                              unsigned char *raw, int *ids, Misc &ms) {
     constexpr int C = kThreads * E;
-    const int V = a.V;
+    const int V = a.V, S = a.S, tid = threadIdx.x;
     float *yb = a.ybuf + (size_t)row * a.ypitch;
     const bool pen = has_penalty(a, p, row);
     uint32_t *cnt = reinterpret_cast<uint32_t *>(raw);
     float mt = kNegInf;
     int at = 0x7fffffff;
     const TIn *src = reinterpret_cast<const TIn *>(a.logits) + (int64_t)row * a.row_stride;
-    for (int c = 0; c < a.S; ++c) {
+    // Final scores into yb, chunk by chunk: E loads per thread (one per element, the
+    // chunk's 256-element rows coalesced), the next chunk's requested before the current
+    // one is penalised and written.  A history of at most kMaxChunksLds ids is kept in
+    // LDS and counted from there per chunk; a longer one is re-read per chunk.
+    const int h0 = pen ? a.hist_off[row] : 0, H = pen ? a.hist_off[row + 1] - h0 : 0;
+    const bool ids_lds = H <= kMaxChunksLds;
+    if (pen && ids_lds) {
+        for (int hb = 0; hb < H; hb += 8 * kThreads) {
+            int id[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) id[j] = a.hist_ids[h0 + min(hb + j * kThreads + tid, H - 1)];
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+                if (hb + j * kThreads + tid < H) ids[hb + j * kThreads + tid] = id[j];
+        }
+    }
+    float xa[E], xb[E];
+    auto request = [&](float (&x)[E], int c) {
         const int c0 = c * C, cn = min(C, V - c0);
-        if (pen) build_counts<C>(cnt, a, row, c0, cn);
-        // eight loads in flight per thread
-        for (int i0 = 0; i0 < cn; i0 += kThreads * 8) {
-            float x[8];
 #pragma unroll
-            for (int j = 0; j < 8; ++j) x[j] = Loader<TIn>::one(src + c0 + min(i0 + j * kThreads + (int)threadIdx.x, cn - 1));
+        for (int j = 0; j < E; ++j) x[j] = Loader<TIn>::one(src + c0 + min(j * kThreads + tid, cn - 1));
+    };
+    request(xa, 0);
+    for (int c = 0; c < S; ++c) {
+        request(xb, min(c + 1, S - 1));
+        const int c0 = c * C, cn = min(C, V - c0);
+        if (pen) {
+            uint4 *c4 = reinterpret_cast<uint4 *>(cnt);
+            for (int i = tid; i < C / 4; i += kThreads) c4[i] = make_uint4(0u, 0u, 0u, 0u);
+            __syncthreads();   // (also: the ids are in LDS)
+            if (ids_lds) {
+                for (int h = tid; h < H; h += kThreads) {
+                    const unsigned rel = (unsigned)(ids[h] - c0);
+                    if (rel < (unsigned)cn) atomicAdd(&cnt[rel], 1u);
+                }
+            } else {
+                for (int hb = tid; hb < H; hb += 8 * kThreads) {
+                    int id[8];
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const int i = i0 + j * kThreads + (int)threadIdx.x;
-                if (i < cn) {
-                    float y = x[j];
-                    if (pen) {
-                        const uint32_t k = cnt[i];
-                        if (k) y = penalize(y, k, p);
+                    for (int j = 0; j < 8; ++j) id[j] = a.hist_ids[h0 + min(hb + j * kThreads, H - 1)];
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) {
+                        const unsigned rel = (unsigned)(id[j] - c0);
+                        if (hb + j * kThreads < H && rel < (unsigned)cn) atomicAdd(&cnt[rel], 1u);
                     }
-                    if (mode != kGreedy) y = __fdiv_rn(y, p.temperature);
-                    yb[c0 + i] = y;
-                    if (y > mt) { mt = y; at = c0 + i; }
                 }
             }
+            __syncthreads();
         }
-        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < E; ++j) {
+            const int i = j * kThreads + tid;
+            if (i < cn) {
+                float y = xa[j];
+                if (pen) {
+                    const uint32_t k = cnt[i];
+                    if (k) y = penalize(y, k, p);
+                }
+                if (mode != kGreedy) y = __fdiv_rn(y, p.temperature);
+                yb[c0 + i] = y;
+                if (y > mt) { mt = y; at = c0 + i; }
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < E; ++j) xa[j] = xb[j];
+        if (pen) __syncthreads();   // the table is read before the next chunk clears it
     }
     const float m = block_max(mt, ms);
     int arg = block_min(mt == m ? at : 0x7fffffff, ms);
@@ -1391,10 +1566,8 @@ __device__ __forceinline__ void dense_resolve(const Args &a, int row, const klsa
         }
         const DenseSource ks{yb, V, cut, cut_idx};
         int last;
-        double before;
-        int tok = ordered_find(
-            V, [&](int i) { const float y = yb[i]; return ks.keep(y, i) ? (double)wfix(y) : 0.0; },
-            (double)p.uniform * (double)zf, ms, last, before);
+        const unsigned long long tgt = (unsigned long long)floor((double)p.uniform * (double)zf);
+        int tok = dense_draw(ks, m, tgt, ms, last);
         if (tok < 0) tok = last >= 0 ? last : 0;
         r.token = tok;
         r.cut = cut;
@@ -1813,36 +1986,73 @@ __device__ __forceinline__ void emit_row(const Args &a, int row, int mode, const
 constexpr int kSpecLoads = 8;    // candidate pairs each thread requests with the chunk summaries
 constexpr int kSpecPairs = 64;   // ... out of the first pairs of each chunk
 
+// The first memory requests of a row's combine: its chunk summaries and the first
+// candidate pairs of its first chunks, in one round trip, issued before the row's
+// parameters are read (they depend on nothing but the launch).  Greedy and full rows
+// without top-N read slots they ignore.
+struct RowSpec {
+    uint4 spec[kSpecLoads];
+    ChunkStat s0;   // the summary of chunk threadIdx.x (clamped)
+};
+
+__device__ __forceinline__ void spec_layout(const Args &a, int &ppc, int &pshift, int &nspec) {
+    ppc = min(a.cand_cap / 2, kSpecPairs);   // a power of two
+    pshift = 31 - __clz(ppc);
+    nspec = min(a.S, (kSpecLoads * kThreads) >> pshift);
+}
+
+// A row's parameters, loaded by every lane from the same address through the vector
+// memory path and made wave-uniform again.  (A scalar load would be waited for together
+// with any other scalar load, e.g. of a kernel argument, issued after it.)
+__device__ __forceinline__ klsample_row_params load_params_vmem(const klsample_row_params *P, int row) {
+    int z;
+    __asm__ volatile("v_mov_b32 %0, 0" : "=v"(z));   // a lane-varying zero: keeps the load a vector load
+    const uint32_t *q = reinterpret_cast<const uint32_t *>(P + row) + z;   // 4-byte aligned
+    uint32_t w[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) w[i] = q[i];
+    klsample_row_params p;
+    static_assert(sizeof(p) == sizeof(w), "row parameters are 32 bytes");
+#pragma unroll
+    for (int i = 0; i < 8; ++i) w[i] = __builtin_amdgcn_readfirstlane(w[i]);
+    __builtin_memcpy(&p, w, sizeof(p));
+    return p;
+}
+
+__device__ __forceinline__ void request_row(const Args &a, int row, RowSpec &r) {
+    int ppc, pshift, nspec;
+    spec_layout(a, ppc, pshift, nspec);
+    const Cand *rc = a.cands + (size_t)row * a.S * a.cand_cap;
+    // (addresses are clamped into range rather than the loads predicated: a predicated
+    // load would be waited for before the next one is issued)
+#pragma unroll
+    for (int i = 0; i < kSpecLoads; ++i) {
+        const int q = threadIdx.x + i * kThreads;
+        const int c = min(q >> pshift, max(nspec - 1, 0));
+        r.spec[i] = reinterpret_cast<const uint4 *>(rc + (size_t)c * a.cand_cap)[q & (ppc - 1)];
+    }
+    r.s0 = load_stat(a.stats + (size_t)row * a.S + min((int)threadIdx.x, a.S - 1));
+}
+
 // Resolve one row from its chunk summaries and candidates.  Runs in one workgroup of
 // kThreads.  Returns false when the candidates cannot settle the row (the caller then
 // runs dense_resolve).
 template <typename TIn, int E>
 __device__ __forceinline__ bool combine_row(const Args &a, int row, const klsample_row_params &p, int mode,
-                                            unsigned char *raw, int *cnt, Misc &ms) {
+                                            const RowSpec &rs, unsigned char *raw, int *cnt, Misc &ms) {
     constexpr int C = kThreads * E;
     const int S = a.S, V = a.V, N = a.N;
-    if ((a.options & KLSAMPLE_OPT_FORCE_DENSE) || S > kMaxChunksLds) return false;
     const int tid = threadIdx.x;
     const ChunkStat *st = a.stats + (size_t)row * S;
     const Cand *rc = a.cands + (size_t)row * S * a.cand_cap;
 
-    // 1. The chunk summaries and the first candidate pairs of the first chunks, requested
-    //    together and independently of the row's parameters: one memory round trip for
-    //    the common row.  (Greedy and full rows without top-N read slots they ignore.)
-    const int ppc = min(a.cand_cap / 2, kSpecPairs);   // a power of two
-    const int pshift = 31 - __clz(ppc);
-    const int nspec = min(S, (kSpecLoads * kThreads) >> pshift);
-    // (addresses are clamped into range rather than the loads predicated: a predicated
-    // load would be waited for before the next one is issued)
-    uint4 spec[kSpecLoads];
-#pragma unroll
-    for (int i = 0; i < kSpecLoads; ++i) {
-        const int q = tid + i * kThreads;
-        const int c = min(q >> pshift, max(nspec - 1, 0));
-        spec[i] = reinterpret_cast<const uint4 *>(rc + (size_t)c * a.cand_cap)[q & (ppc - 1)];
-    }
+    // 1. The chunk summaries and the first candidate pairs of the first chunks (requested
+    //    by the caller, request_row)
+    int ppc, pshift, nspec;
+    spec_layout(a, ppc, pshift, nspec);
+    const uint4 *spec = rs.spec;
     const bool has = tid < S;
-    const ChunkStat s0 = load_stat(st + min(tid, S - 1));
+    const ChunkStat s0 = rs.s0;
 
     // 2. Row max, candidate bound, finite count, overflow (bit 0) and whether any chunk
     //    has candidates past the requested slots (bit 1); then sum-exp and argmax.
@@ -2244,15 +2454,10 @@ struct ScanLds {
 // dense work that follows (bound, candidates, sums) sees final scores everywhere
 // with no per-element branch.
 template <typename TIn, int E, bool kVec>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(E >= 32 ? 6 : E >= 16 ? 7 : 8))) void scan_kernel(Args a) {
+__device__ __forceinline__ void scan_chunk(const Args &a, int row, int chunk, unsigned char *raw, ScanMisc &ms) {
     constexpr int VW = Loader<TIn>::VW;
     constexpr int NV = E / VW;
     constexpr int C = kThreads * E;
-    __shared__ __attribute__((aligned(16))) unsigned char raw[ScanLds<E>::value];
-    __shared__ ScanMisc ms;
-
-    int row, chunk;
-    map_block(a, row, chunk);
     const klsample_row_params p = a.params[row];
     const int V = a.V;
     const int tid = threadIdx.x;
@@ -2267,11 +2472,14 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(E >= 3
     // the count table is built while the logits are in flight.  Counts are 16-bit
     // halves of LDS words (exact below 65536 ids); longer histories take the 32-bit
     // path below.
+    // (the offsets are requested with the parameters, not after them: one memory round
+    // trip before the loads start)
     int h0 = 0, h1 = 0;
-    if ((p.flags & (KLSAMPLE_ROW_REPETITION | KLSAMPLE_ROW_PRESENCE_FREQUENCY)) && a.hist_off != nullptr) {
+    if (a.hist_off != nullptr) {
         h0 = a.hist_off[row];
         h1 = a.hist_off[row + 1];
     }
+    if (!(p.flags & (KLSAMPLE_ROW_REPETITION | KLSAMPLE_ROW_PRESENCE_FREQUENCY))) h1 = h0;
     const int H = h1 - h0;
     // 16-bit counts (two per word) cover the chunk when no count can reach 65536;
     // longer histories count in 32 bits over each half of the chunk in turn
@@ -2549,6 +2757,15 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(E >= 3
     }
 }
 
+template <typename TIn, int E, bool kVec>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(E >= 32 ? 6 : E >= 16 ? 7 : 8))) void scan_kernel(Args a) {
+    __shared__ __attribute__((aligned(16))) unsigned char raw[ScanLds<E>::value];
+    __shared__ ScanMisc ms;
+    int row, chunk;
+    map_block(a, row, chunk);
+    scan_chunk<TIn, E, kVec>(a, row, chunk, raw, ms);
+}
+
 template <int C>
 struct RowLds {
     static constexpr int a = C * 4;
@@ -2556,17 +2773,30 @@ struct RowLds {
     static constexpr int value = a > b ? a : b;
 };
 
-// One workgroup per row: combine the chunk candidates, or run the multi-pass path.
+// One row in one workgroup: combine the chunk candidates, or run the multi-pass path.
+// `raw` holds RowLds<C>::value bytes, `cnt` kMaxChunksLds ints.
+template <typename TIn, int E>
+__device__ __forceinline__ void row_body(const Args &a, int row, unsigned char *raw, int *cnt, Misc &ms) {
+    // the row's first loads go out before its parameters arrive (which are read through
+    // the vector memory path, so that waiting for them waits for nothing else)
+    RowSpec rs;
+    request_row(a, row, rs);
+    const klsample_row_params p = load_params_vmem(a.params, row);
+    const int mode = row_mode(p, a.V);
+    if ((a.options & KLSAMPLE_OPT_FORCE_DENSE) || a.S > kMaxChunksLds ||
+        !combine_row<TIn, E>(a, row, p, mode, rs, raw, cnt, ms)) {
+        __syncthreads();   // the combine's LDS (cnt included) is reused
+        dense_resolve<TIn, E>(a, row, p, mode, raw, cnt, ms);
+    }
+}
+
 template <typename TIn, int E>
 __global__ __launch_bounds__(kThreads) void row_kernel(Args a) {
     constexpr int C = kThreads * E;
     __shared__ __attribute__((aligned(16))) unsigned char raw[RowLds<C>::value];
     __shared__ int cnt[kMaxChunksLds];
     __shared__ Misc ms;
-    const int row = blockIdx.x;
-    const klsample_row_params p = a.params[row];
-    const int mode = row_mode(p, a.V);
-    if (!combine_row<TIn, E>(a, row, p, mode, raw, cnt, ms)) dense_resolve<TIn, E>(a, row, p, mode, raw, ms);
+    row_body<TIn, E>(a, blockIdx.x, raw, cnt, ms);
 }
 
 // Final probabilities: exp(s - max - log_norm) on the kept set, 0 elsewhere.
@@ -2612,7 +2842,8 @@ hipError_t launch_typed(const Args &a, hipStream_t s, const PhaseEvents *ph) {
     if (e != hipSuccess) return e;
     // 16-byte loads need aligned rows and a last chunk of at least one vector
     const int tail = a.V - (a.S - 1) * a.C;
-    if (a.vec_ok && tail * (int)sizeof(TIn) >= 16) scan_kernel<TIn, E, true><<<grid, kThreads, 0, s>>>(a);
+    const bool vec = a.vec_ok && tail * (int)sizeof(TIn) >= 16;
+    if (vec) scan_kernel<TIn, E, true><<<grid, kThreads, 0, s>>>(a);
     else scan_kernel<TIn, E, false><<<grid, kThreads, 0, s>>>(a);
     if ((e = mark(ph, 1, s)) != hipSuccess) return e;
     row_kernel<TIn, E><<<dim3((unsigned)a.B), kThreads, 0, s>>>(a);

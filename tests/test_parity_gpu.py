@@ -153,11 +153,13 @@ def test_vocab_sizes_and_modes(vocab, dtype):
     check(out, rows, params, probs=True)
 
 
+@pytest.mark.parametrize('dense', [False, True])
 @pytest.mark.parametrize('dtype', [torch.float32, torch.bfloat16])
-def test_long_histories_count_past_16_bits(dtype):
+def test_long_histories_count_past_16_bits(dtype, dense):
     """Histories of 65536 ids or more take 32-bit counts over each half of a chunk in
-    turn; an id repeated more than 65535 times keeps its exact count."""
-    say(f'long histories dtype={dtype}')
+    turn; an id repeated more than 65535 times keeps its exact count.  Forced through the
+    multi-pass row path, a history this long is re-read per chunk rather than kept in LDS."""
+    say(f'long histories dtype={dtype} dense={dense}')
     rng = np.random.default_rng(12)
     V = 151936
     kinds = ['greedy', 'topk', 'topp', 'full'] * 2
@@ -178,7 +180,9 @@ def test_long_histories_count_past_16_bits(dtype):
     # the hot id's penalty depends on its full count: 66000 * 2e-5 moves it by 1.32
     u = rng.random(len(kinds)).astype(np.float32)
     rows = sample_rows(logits, hist, params, u)
-    out = run(logits, params, hist, u, probs=True)
+    out = run(logits, params, hist, u, probs=True, options=_lib.OPT_FORCE_DENSE if dense else 0)
+    if dense:
+        assert (out.info['path'] == 1).all()
     check(out, rows, params, probs=True)
 
 
