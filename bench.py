@@ -402,7 +402,7 @@ def summarize_pmc(fetch_root, write_root, command_fetch, command_write):
         (fv, nf), (wv, nw) = fa.get(key, (0.0, 0)), wa.get(key, (0.0, 0))
         scaled = int(round((fv * ff + wv * fw) * 1024))
         lines.append(f'| {key[0]} | {key[1]} | {nf}/{nw} | {fv:.0f} | {wv:.0f} | {scaled} |')
-        if key[0].startswith('scan_kernel<float,32>'):
+        if key[0].startswith('scan_kernel<float,32'):   # the headline's (fp32, 32 elements per thread)
             traffic = scaled
     lines.append('')
     if traffic is not None:

@@ -84,7 +84,9 @@ bool make_plan(int32_t batch, int32_t vocab, int32_t dtype, int32_t max_top_k, i
     p->off_stats = off;   off = align_up(off + B * S * sizeof(ChunkStat), 256);
     p->off_cands = off;   off = align_up(off + B * S * (size_t)cap * sizeof(Cand), 256);
     p->off_rows = off;    off = align_up(off + B * sizeof(klsample_row_info), 256);
-    p->ypitch = (int32_t)align_up((size_t)vocab, 4);   // ybuf rows start 16-byte aligned
+    // ybuf rows start 16-byte aligned; the last float of a row is a spare slot that no
+    // pass reads (they read up to vocab rounded up to 4)
+    p->ypitch = (int32_t)align_up((size_t)vocab + 1, 4);
     p->off_ybuf = off;    off = align_up(off + B * (size_t)p->ypitch * sizeof(float), 256);
     p->total = off;
     return (int64_t)batch * p->chunks <= INT32_MAX;

@@ -68,7 +68,7 @@ struct Args {
     Cand *cands;           // per (row, chunk): cand_cap slots
     klsample_row_info *rows;
     float *ybuf;           // dense row path: per row ypitch final scores
-    int32_t ypitch;        // vocab rounded up to a multiple of 4
+    int32_t ypitch;        // vocab + 1 rounded up to a multiple of 4 (the last float is a spare slot)
     int32_t E, C, S, cand_cap;
     int32_t vec_ok;   // 16-byte vector loads are legal for every row
     int32_t xcd_map;  // place all chunks of a row on one XCD

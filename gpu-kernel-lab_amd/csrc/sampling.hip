@@ -1436,6 +1436,7 @@ __device__ __forceinline__ void dense_resolve(const Args &a, int row, const klsa
                 if (hb + j * kThreads + tid < H) ids[hb + j * kThreads + tid] = id[j];
         }
     }
+    const int spare = a.ypitch - 1;   // past every position a pass reads
     float xa[E], xb[E];
     auto request = [&](float (&x)[E], int c) {
         const int c0 = c * C, cn = min(C, V - c0);
@@ -1469,19 +1470,21 @@ __device__ __forceinline__ void dense_resolve(const Args &a, int row, const klsa
             }
             __syncthreads();
         }
+        // the counts first (one LDS wait), then the scores; every thread stores E values
+        // (positions past the chunk go to the row's spare slot), so no branch separates
+        // the stores from the loads in flight
+        uint32_t kc[E];
+#pragma unroll
+        for (int j = 0; j < E; ++j) kc[j] = pen ? cnt[j * kThreads + tid] : 0u;
 #pragma unroll
         for (int j = 0; j < E; ++j) {
             const int i = j * kThreads + tid;
-            if (i < cn) {
-                float y = xa[j];
-                if (pen) {
-                    const uint32_t k = cnt[i];
-                    if (k) y = penalize(y, k, p);
-                }
-                if (mode != kGreedy) y = __fdiv_rn(y, p.temperature);
-                yb[c0 + i] = y;
-                if (y > mt) { mt = y; at = c0 + i; }
-            }
+            float y = xa[j];
+            if (kc[j]) y = penalize(y, kc[j], p);
+            if (mode != kGreedy) y = __fdiv_rn(y, p.temperature);
+            const bool in = i < cn;
+            yb[in ? c0 + i : spare] = y;
+            if (in && y > mt) { mt = y; at = c0 + i; }
         }
 #pragma unroll
         for (int j = 0; j < E; ++j) xa[j] = xb[j];
