@@ -234,6 +234,9 @@ __device__ __forceinline__ T block_reduce(T v, Op op, T *scratch, T id) {
 }
 
 struct OpMaxF { __device__ float operator()(float a, float b) const { return fmaxf(a, b); } };
+struct OpMaxQ {
+    __device__ unsigned long long operator()(unsigned long long a, unsigned long long b) const { return a > b ? a : b; }
+};
 struct OpMinI { __device__ int operator()(int a, int b) const { return a < b ? a : b; } };
 struct OpMaxI { __device__ int operator()(int a, int b) const { return a > b ? a : b; } };
 struct OpSumI { __device__ int operator()(int a, int b) const { return a + b; } };
@@ -2282,11 +2285,74 @@ __device__ __forceinline__ bool combine_row(const Args &a, int row, const klsamp
         // candidate whose quotient reaches it (ties created by the division included),
         // divided and sorted in final space.
         const int kk = p.top_k;
+        // the top set Es[0..lk) sorted in final space, with vocab-order ranks in ms.irank:
+        // one wave applies top-p and finishes
+        auto finish_top = [&](const unsigned long long *Es, int lk) {
+            if (wave_id() == 0) {
+                const double mref = (double)desc_key_y(Es[0]);
+                int L = lk;
+                if (p.flags & KLSAMPLE_ROW_TOP_P) {
+                    const double w = lane_id() < lk ? (double)__expf(desc_key_y(Es[lane_id()]) - (float)mref) : 0.0;
+                    const int cut = wave_topp(Es, lk, mref, wave_reduce(w, OpSumD(), 0.0), p.top_p);
+                    if (cut > 0) L = cut;
+                }
+                wave_finish(a, row, mode, p, Es, lk, L, mref, A, ms.irank, true);
+            }
+        };
         if (nF > kk && N <= 64) {
             // one histogram pass isolates the kk best; sorted, they give the kk-th
             // quotient, and the top set (every candidate whose quotient reaches it) is
             // gathered, divided and sorted; one wave applies top-p and finishes
             const int t = hist_gather(A, nF, kk, ylo, yhi, D, kSortCap, ms, narrowed);
+            if (t >= kk && t <= 64) {
+                // The gather holds the kk best and at most 64 entries in all: every wave
+                // finds the kk-th best itself (the worst entry dropped t - kk times; no
+                // barrier).  Every candidate scoring at least the smallest gathered score
+                // is in the gather (its bin is at or above that one's), so when the kk-th
+                // quotient's threshold xt is no lower than that score, the top set is the
+                // gathered entries scoring >= xt.  -inf and signed zeros go the long way.
+                const int l = lane_id();
+                unsigned long long kl = l < t ? D[l] : 0ull;   // 0: never the worst
+                unsigned long long kw = wave_reduce(kl, OpMaxQ(), 0ull);
+                const float xmin = desc_key_y(kw);
+                for (int r = kk; r < t; ++r) {
+                    if (kl == kw) kl = 0ull;   // keys are distinct: drops one entry
+                    kw = wave_reduce(kl, OpMaxQ(), 0ull);
+                }
+                const float xk = desc_key_y(kw);
+                const float xt = (xk > kNegInf && xk != 0.f)
+                                     ? quotient_threshold(__fdiv_rn(xk, p.temperature), p.temperature)
+                                     : kNegInf;
+                if (xk > kNegInf && xk != 0.f && xt >= xmin) {
+                    const bool in = l < t && desc_key_y(D[l]) >= xt;
+                    const unsigned long long bal = __ballot(in);
+                    const int lk = __popcll(bal);
+                    // final-space keys of the top set, into a copy (other waves may still
+                    // be reading D)
+                    const unsigned long long *Ef = D;
+                    if (p.temperature != 1.f || lk < t) {
+                        unsigned long long *Eq = D + 256;
+                        if (wave_id() == 0 && in) {
+                            const int pos = __builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32),
+                                                                      __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0u));
+                            Eq[pos] = desc_key(__fdiv_rn(desc_key_y(D[l]), p.temperature), desc_key_idx(D[l]));
+                        }
+                        __syncthreads();
+                        Ef = Eq;
+                    }
+                    const unsigned long long *Es = Ef;
+                    if (lk > 1) {
+                        unsigned long long *Eo = D + 128;
+                        block_rank_sort_idx(Ef, lk, Eo, ms.part, ms.irank);
+                        Es = Eo;
+                    } else {
+                        if (tid == 0) ms.irank[0] = 0u;
+                        __syncthreads();
+                    }
+                    finish_top(Es, lk);
+                    return true;
+                }
+            }
             if (t >= kk && t <= 256) {
                 block_rank_sort(D, t, ms.part);
                 const float xt = quotient_threshold(__fdiv_rn(desc_key_y(D[kk - 1]), p.temperature), p.temperature);
@@ -2312,16 +2378,7 @@ __device__ __forceinline__ bool combine_row(const Args &a, int row, const klsamp
                         ms.irank[0] = 0u;
                     }
                     if (lk <= 1) __syncthreads();
-                    if (wave_id() == 0) {
-                        const double mref = (double)desc_key_y(Es[0]);
-                        int L = lk;
-                        if (p.flags & KLSAMPLE_ROW_TOP_P) {
-                            const double w = lane_id() < lk ? (double)__expf(desc_key_y(Es[lane_id()]) - (float)mref) : 0.0;
-                            const int cut = wave_topp(Es, lk, mref, wave_reduce(w, OpSumD(), 0.0), p.top_p);
-                            if (cut > 0) L = cut;
-                        }
-                        wave_finish(a, row, mode, p, Es, lk, L, mref, A, ms.irank, true);
-                    }
+                    finish_top(Es, lk);
                     return true;
                 }
             }
