@@ -136,6 +136,7 @@ struct Misc : Red {
     uint32_t part[kThreads];   // block_rank_sort: per-thread partial ranks
     uint32_t irank[64];        // block_index_rank: vocab-order ranks of a kept list
     unsigned long long hmass[256];
+    unsigned long long sink[kThreads];   // per-thread target of masked LDS stores
     int topn_idx[kMaxLogprobs];
     float topn_y[kMaxLogprobs];
     uint32_t bound_key;
@@ -1932,9 +1933,13 @@ __device__ __forceinline__ int hist_gather(const unsigned long long *A, int n, i
         key[j] = A[min(i, n - 1)];
         bn[j] = (i < n) ? bin(key[j]) : -1;
     }
+    // rounds past n are skipped by the whole block; in the last one, lanes past n add 0
+    // (no per-entry branch)
 #pragma unroll
-    for (int j = 0; j < kPer; ++j)
-        if (bn[j] >= 0) atomicAdd(&ms.hist[bn[j]], 1u);
+    for (int j = 0; j < kPer; ++j) {
+        if (j * kThreads >= n) break;
+        atomicAdd(&ms.hist[max(bn[j], 0)], bn[j] >= 0 ? 1u : 0u);
+    }
     __syncthreads();
     const int l = lane_id();
     uint32_t c[4], sum = 0u;
@@ -1961,12 +1966,13 @@ __device__ __forceinline__ int hist_gather(const unsigned long long *A, int n, i
     int base = 0;
     if (l == 63 && pincl > 0) base = atomicAdd(&ms.ib, pincl);
     base = readlane(base, 63) + pincl - mine;
+    unsigned long long *const sink = &ms.sink[threadIdx.x];
 #pragma unroll
-    for (int j = 0; j < kPer; ++j) {
-        if (bn[j] >= b) {
-            if (base < cap) D[base] = key[j];
-            ++base;
-        }
+    for (int j = 0; j < kPer; ++j) {   // branch-free: the others go to the thread's sink
+        if (j * kThreads >= n) break;
+        const bool ok = bn[j] >= b;
+        *((ok && base < cap) ? &D[base] : sink) = key[j];
+        base += ok ? 1 : 0;
     }
     __syncthreads();
     return ms.ib;
@@ -2136,13 +2142,15 @@ __device__ __forceinline__ bool combine_row(const Args &a, int row, const klsamp
         // slot rounds whose first chunk is past the requested ones are skipped by the
         // whole wave
         const int wq0 = __builtin_amdgcn_readfirstlane(wave_id() * 64);
+        int ncs[kSpecLoads];
+#pragma unroll
+        for (int i = 0; i < kSpecLoads; ++i)   // all counts read before any is used
+            ncs[i] = cnt[min((tid + i * kThreads) >> pshift, kMaxChunksLds - 1)];
 #pragma unroll
         for (int i = 0; i < kSpecLoads; ++i) {
             if (((wq0 + i * kThreads) >> pshift) >= nspec) break;
             const int q = tid + i * kThreads;
-            const int c = q >> pshift;
-            const int nc0 = cnt[min(c, kMaxChunksLds - 1)];   // read unconditionally
-            const int nc = (c < nspec) ? nc0 : 0, j = 2 * (q & (ppc - 1));
+            const int nc = ((q >> pshift) < nspec) ? ncs[i] : 0, j = 2 * (q & (ppc - 1));
             if (j < nc && __uint_as_float(spec[i].x) >= xs) acc |= 1u << (2 * i);
             if (j + 1 < nc && __uint_as_float(spec[i].z) >= xs) acc |= 2u << (2 * i);
         }
@@ -2151,21 +2159,22 @@ __device__ __forceinline__ bool combine_row(const Args &a, int row, const klsamp
         int base = 0;
         if (lane_id() == 63 && incl > 0) base = atomicAdd(&ms.ncand, incl);
         base = readlane(base, 63) + incl - mine;
+        // branch-free: every slot is stored, the rejected ones (and any past the list's
+        // capacity) to the thread's sink; a taken branch per slot costs more
+        unsigned long long *const sink = &ms.sink[tid];
+        auto put = [&](bool ok, float y, int idx) {
+            unsigned long long *dst = (ok && base < kSortCap) ? &A[base] : sink;
+            *dst = desc_key(y, idx);
+            base += ok ? 1 : 0;
+            const uint32_t k = fkey(y);
+            kmin = ok ? min(kmin, k) : kmin;
+            kmax = ok ? max(kmax, k) : kmax;
+        };
 #pragma unroll
         for (int i = 0; i < kSpecLoads; ++i) {
             if (((wq0 + i * kThreads) >> pshift) >= nspec) break;
-            if (acc & (1u << (2 * i))) {
-                if (base < kSortCap) A[base] = desc_key(__uint_as_float(spec[i].x), (int)spec[i].y);
-                ++base;
-                const uint32_t k = fkey(__uint_as_float(spec[i].x));
-                kmin = min(kmin, k); kmax = max(kmax, k);
-            }
-            if (acc & (2u << (2 * i))) {
-                if (base < kSortCap) A[base] = desc_key(__uint_as_float(spec[i].z), (int)spec[i].w);
-                ++base;
-                const uint32_t k = fkey(__uint_as_float(spec[i].z));
-                kmin = min(kmin, k); kmax = max(kmax, k);
-            }
+            put((acc >> (2 * i)) & 1u, __uint_as_float(spec[i].x), (int)spec[i].y);
+            put((acc >> (2 * i + 1)) & 1u, __uint_as_float(spec[i].z), (int)spec[i].w);
         }
     }
     if (need_rest) {
