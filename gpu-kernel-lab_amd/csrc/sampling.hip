@@ -1780,7 +1780,7 @@ __device__ __forceinline__ void wave_finish(const Args &a, int row, int mode, co
     r.cut = readlane(y, L - 1);
     r.cut_idx = (L < n && desc_key_y(D[L]) == r.cut) ? __builtin_amdgcn_readlane(idx, L - 1) : a.V;
     r.kept = L;
-    r.log_norm = log(zf);
+    r.log_norm = (double)logf((float)zf);   // zf >= 1: float accuracy (~1e-7 absolute) suffices
     __builtin_amdgcn_wave_barrier();
     if (placed) {
         scr[rank] = __double_as_longlong(w);
@@ -1893,6 +1893,7 @@ __device__ __forceinline__ int select_top(const unsigned long long *A, int n, in
 // distance from it is a few ulps; +inf when no finite x qualifies, -inf for y = -inf.
 __device__ __forceinline__ float quotient_threshold(float y, float T) {
     if (!(y > kNegInf)) return kNegInf;
+    if (T == 1.f) return y;   // fl(x / 1) = x
     float x = __fmul_rn(y, T);
     if (!(fabsf(x) <= __FLT_MAX__)) x = x > 0.f ? __FLT_MAX__ : -__FLT_MAX__;
     for (int i = 0; i < 64 && !(__fdiv_rn(x, T) >= y); ++i) {
