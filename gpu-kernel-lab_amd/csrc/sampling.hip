@@ -2435,8 +2435,21 @@ __device__ __forceinline__ bool combine_row(const Args &a, int row, const klsamp
     // top-p alone: the best 64 (one wave), then the best 256, then every candidate
     const double mref = (double)m;
     if (nF > 64 && N <= 64) {
-        const int t = hist_gather(A, nF, 64, ylo, yhi, D, kSortCap, ms, narrowed);
-        if (t >= 0 && t <= 256) {
+        // the best 63 (and the ties of their bin): usually at most 64 entries, sorted
+        // with their vocab-order ranks in one block pass; one wave applies top-p and
+        // finishes (entries past the cut draw with weight 0)
+        const int t = hist_gather(A, nF, 63, ylo, yhi, D, kSortCap, ms, narrowed);
+        if (t >= 2 && t <= 64) {
+            unsigned long long *Eo = D + 128;
+            block_rank_sort_idx(D, t, Eo, ms.part, ms.irank);
+            if (wave_id() == 0) {
+                const int cut = wave_topp(Eo, t, mref, Z, p.top_p);
+                if (cut > 0) wave_finish(a, row, mode, p, Eo, t, cut, mref, A, ms.irank, true);
+                if (lane_id() == 0) ms.flag = cut;
+            }
+            __syncthreads();
+            if (ms.flag > 0) return true;
+        } else if (t >= 0 && t <= 256) {
             block_rank_sort(D, t, ms.part);
             if (wave_id() == 0) {
                 const int cut = wave_topp(D, min(t, 64), mref, Z, p.top_p);
