@@ -277,6 +277,35 @@ def test_large_top_k_and_top_n():
     check(out, rows, params)
 
 
+def test_top_k_quotient_ties():
+    """Distinct scores one ulp apart around the k-th collapse to equal quotients after the
+    division by T: the top set takes every candidate whose quotient reaches the k-th one,
+    including scores below the k-th best (the combine's short path must step aside)."""
+    say('top-k quotient ties')
+    rng = np.random.default_rng(21)
+    V, B = 30011, 24
+    x = (rng.standard_normal((B, V)) * 2).astype(np.float32)
+    params, u = [], rng.random(B).astype(np.float32)
+    for b in range(B):
+        k = int(rng.integers(5, 60))
+        # a run of consecutive floats placed across the k-th largest position
+        top = np.sort(x[b])[::-1]
+        base = np.float32(top[k - 1] + 1.0)
+        run_len = int(rng.integers(3, 12))
+        vals = np.nextafter(np.full(run_len, base), np.float32(-np.inf))
+        for j in range(1, run_len):
+            vals[j] = np.nextafter(vals[j - 1], np.float32(-np.inf))
+        pos = rng.choice(V, run_len + k, replace=False)
+        x[b, pos[:k - 2]] = base + np.float32(5.0) + rng.random(k - 2).astype(np.float32)
+        x[b, pos[k:k + run_len]] = vals
+        t = float(rng.choice([7.0, 7.0, 5.0, 3.0, 0.3, 1.7, 1.0]))
+        params.append(SamplingParams(temperature=t, top_k=k, top_p=float(rng.choice([1.0, 0.9, 0.5])), logprobs=4))
+    logits = torch.from_numpy(x)
+    rows = sample_rows(logits, None, params, u)
+    out = run(logits, params, None, u, probs=True)
+    check(out, rows, params, probs=True)
+
+
 @pytest.mark.parametrize('elems', ['4', '8', '16'])
 def test_other_chunk_sizes(elems, monkeypatch):
     """The smaller chunk variants (selected by KLSAMPLE_ELEMS_PER_THREAD, read per call)
