@@ -64,9 +64,14 @@ __device__ __forceinline__ float exp_fast(float d) {
 }
 
 // Fixed-point weight (unit 2^-40) of a final score y under the row max m: integer sums
-// are exact and independent of their order.
+// are exact and independent of their order.  w * 2^40 (w = exp(y - m) <= 1) is exact in
+// fp32, rounded half-to-even to an integer there, and split into two 32-bit halves, each
+// converted exactly: the value of round((double)w * 2^40), in full-rate fp32 operations.
 __device__ __forceinline__ unsigned long long weight_fix(float y, float m) {
-    return (unsigned long long)__double2ull_rn((double)exp_fast(y - m) * kFixScale);
+    const float f = __builtin_rintf(exp_fast(y - m) * 1099511627776.0f);
+    const float h = __builtin_truncf(f * 2.3283064365386963e-10f);   // f / 2^32
+    const float lo = __builtin_fmaf(h, -4294967296.0f, f);            // f - h * 2^32, exact
+    return ((unsigned long long)(uint32_t)h << 32) | (uint32_t)lo;
 }
 
 __device__ __forceinline__ int row_mode(const klsample_row_params &p, int V) {
