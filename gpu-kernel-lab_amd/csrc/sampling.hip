@@ -2001,6 +2001,7 @@ __device__ __forceinline__ void emit_row(const Args &a, int row, int mode, const
     write_row(a, row, mode, r, count, ms);
 }
 
+constexpr int kTopPShort = 48;   // top-p rows first try a kept set within their best 48
 constexpr int kSpecLoads = 8;    // candidate pairs each thread requests with the chunk summaries
 constexpr int kSpecPairs = 64;   // ... out of the first pairs of each chunk
 
@@ -2440,21 +2441,33 @@ __device__ __forceinline__ bool combine_row(const Args &a, int row, const klsamp
     // top-p alone: the best 64 (one wave), then the best 256, then every candidate
     const double mref = (double)m;
     if (nF > 64 && N <= 64) {
-        // the best 63 (and the ties of their bin): usually at most 64 entries, sorted
-        // with their vocab-order ranks in one block pass; one wave applies top-p and
-        // finishes (entries past the cut draw with weight 0)
-        const int t = hist_gather(A, nF, 63, ylo, yhi, D, kSortCap, ms, narrowed);
-        if (t >= 2 && t <= 64) {
-            unsigned long long *Eo = D + 128;
-            block_rank_sort_idx(D, t, Eo, ms.part, ms.irank);
-            if (wave_id() == 0) {
-                const int cut = wave_topp(Eo, t, mref, Z, p.top_p);
-                if (cut > 0) wave_finish(a, row, mode, p, Eo, t, cut, mref, A, ms.irank, true);
-                if (lane_id() == 0) ms.flag = cut;
+        // First the best 48 (and the ties of their bin): when that is at most 64 entries
+        // they are sorted with their vocab-order ranks in one block pass and one wave
+        // applies top-p and finishes (entries past the cut draw with weight 0), if the
+        // kept set lies within them.  Otherwise the best 64 below.
+        bool dirty = narrowed;
+        if (nF > kTopPShort) {
+            const int t = hist_gather(A, nF, kTopPShort, ylo, yhi, D, kSortCap, ms, dirty);
+            dirty = true;
+            if (t >= 2 && t <= 64) {
+                unsigned long long *Eo = D + 128;
+                block_rank_sort_idx(D, t, Eo, ms.part, ms.irank);
+                if (wave_id() == 0) {
+                    const int cut = wave_topp(Eo, t, mref, Z, p.top_p);
+                    if (cut > 0) wave_finish(a, row, mode, p, Eo, t, cut, mref, A, ms.irank, true);
+                    if (lane_id() == 0) ms.flag = cut;
+                }
+                __syncthreads();
+                if (ms.flag > 0) return true;
             }
+        }
+        if (dirty) {
+            __syncthreads();   // every wave has read the first gather's count
+            if (threadIdx.x == 0) ms.ib = 0;   // hist_gather's counter
             __syncthreads();
-            if (ms.flag > 0) return true;
-        } else if (t >= 0 && t <= 256) {
+        }
+        const int t = hist_gather(A, nF, 64, ylo, yhi, D, kSortCap, ms, dirty);
+        if (t >= 0 && t <= 256) {
             block_rank_sort(D, t, ms.part);
             if (wave_id() == 0) {
                 const int cut = wave_topp(D, min(t, 64), mref, Z, p.top_p);
