@@ -306,6 +306,28 @@ def test_top_k_quotient_ties():
     check(out, rows, params, probs=True)
 
 
+def test_top_p_kept_sets_around_the_short_list():
+    """Top-p rows whose kept set has 30 to 80 entries: within the combine's first (best-48)
+    list, just past it (second gather of the best 64), and past both (general path)."""
+    say('top-p kept sets around 48 and 64')
+    rng = np.random.default_rng(22)
+    V = 151936
+    heads = [30, 40, 46, 48, 50, 55, 60, 63, 64, 66, 72, 80]
+    x = (rng.standard_normal((len(heads), V))).astype(np.float32)
+    params = []
+    for b, h in enumerate(heads):
+        pos = rng.choice(V, h, replace=False)
+        x[b, pos] = (12.0 + 0.05 * rng.standard_normal(h)).astype(np.float32)
+        params.append(SamplingParams(temperature=1.0, top_p=float(rng.choice([0.9, 0.97, 0.995])), logprobs=3))
+    u = rng.random(len(heads)).astype(np.float32)
+    logits = torch.from_numpy(x)
+    for dt in (torch.float32, torch.bfloat16):
+        lt = logits.to(dt)
+        rows = sample_rows(lt, None, params, u)
+        out = run(lt, params, None, u, probs=True)
+        check(out, rows, params, probs=True)
+
+
 @pytest.mark.parametrize('elems', ['4', '8', '16'])
 def test_other_chunk_sizes(elems, monkeypatch):
     """The smaller chunk variants (selected by KLSAMPLE_ELEMS_PER_THREAD, read per call)
