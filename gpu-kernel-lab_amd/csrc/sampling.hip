@@ -1757,7 +1757,7 @@ __device__ __forceinline__ void wave_write(const Args &a, int row, int mode, con
 __device__ __forceinline__ void wave_finish(const Args &a, int row, int mode, const klsample_row_params &p,
                                             const unsigned long long *D, int n, int L, double mref,
                                             unsigned long long *scr, const uint32_t *irank = nullptr,
-                                            bool ranked_all = false) {
+                                            bool ranked_all = false, const double *wz = nullptr) {
     const int l = lane_id();
     const bool kept = l < L;
     // ranked_all: irank holds vocab-order ranks among all n <= 64 entries; the entries
@@ -1766,7 +1766,8 @@ __device__ __forceinline__ void wave_finish(const Args &a, int row, int mode, co
     const unsigned long long key = placed ? D[l] : ~0ull;
     const float y = placed ? desc_key_y(key) : kNegInf;
     const int idx = placed ? desc_key_idx(key) : 0x7fffffff;
-    const double w = kept ? (double)__expf(y - (float)mref) : 0.0;
+    // wz (optional): the lane's weight and the kept sum, already computed by the caller
+    const double w = wz ? (kept ? wz[0] : 0.0) : (kept ? (double)__expf(y - (float)mref) : 0.0);
     int rank = 0;
     if (irank != nullptr) {
         rank = placed ? (int)irank[l] : 0;
@@ -1778,7 +1779,7 @@ __device__ __forceinline__ void wave_finish(const Args &a, int row, int mode, co
             rank += (j + 1 < L && desc_key_idx(q.y) < idx) ? 1 : 0;
         }
     }
-    const double zf = wave_reduce(w, OpSumD(), 0.0);
+    const double zf = wz ? wz[1] : wave_reduce(w, OpSumD(), 0.0);
     RowOut r;
     r.path = 0;
     r.m = (float)mref;
@@ -2305,14 +2306,21 @@ __device__ __forceinline__ bool combine_row(const Args &a, int row, const klsamp
         // one wave applies top-p and finishes
         auto finish_top = [&](const unsigned long long *Es, int lk) {
             if (wave_id() == 0) {
-                const double mref = (double)desc_key_y(Es[0]);
+                // the weights and one prefix scan serve the top-p cut and the kept sum
+                const int l = lane_id();
+                const float y0 = desc_key_y(Es[0]);
+                const double mref = (double)y0;
+                const double w = l < lk ? (double)__expf(desc_key_y(Es[l]) - y0) : 0.0;
+                const double incl = wave_incl_scan(w);
                 int L = lk;
                 if (p.flags & KLSAMPLE_ROW_TOP_P) {
-                    const double w = lane_id() < lk ? (double)__expf(desc_key_y(Es[lane_id()]) - (float)mref) : 0.0;
-                    const int cut = wave_topp(Es, lk, mref, wave_reduce(w, OpSumD(), 0.0), p.top_p);
-                    if (cut > 0) L = cut;
+                    const double z = readlane(incl, lk - 1);
+                    const unsigned long long cross = __ballot(l < lk && wave_shift_excl(incl) > (double)p.top_p * z);
+                    if (cross) L = __ffsll((long long)cross) - 1;
+                    if (L < 1) L = lk;
                 }
-                wave_finish(a, row, mode, p, Es, lk, L, mref, A, ms.irank, true);
+                const double wz[2] = {w, readlane(incl, L - 1)};
+                wave_finish(a, row, mode, p, Es, lk, L, mref, A, ms.irank, true, wz);
             }
         };
         if (nF > kk && N <= 64) {
