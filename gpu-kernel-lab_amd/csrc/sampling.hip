@@ -1753,7 +1753,8 @@ __device__ __forceinline__ void wave_write(const Args &a, int row, int mode, con
 // Finish a sampled row in one wave: D[0..n) sorted best first, the first L kept
 // (1 <= L <= 64, L <= n), N <= 64; `scr` is 128 free LDS words of 8 bytes.  Same
 // results as finish_sampled.  The draw ranks the kept entries by vocab index (broadcast
-// LDS reads), places their weights in index order and takes one prefix scan.
+// LDS reads, or `irank`), places their weights in index order and takes one prefix scan.
+// `wz`, when given, holds the lane's weight exp(y - mref) and the kept entries' sum.
 __device__ __forceinline__ void wave_finish(const Args &a, int row, int mode, const klsample_row_params &p,
                                             const unsigned long long *D, int n, int L, double mref,
                                             unsigned long long *scr, const uint32_t *irank = nullptr,
