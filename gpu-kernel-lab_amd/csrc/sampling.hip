@@ -2830,12 +2830,12 @@ __device__ __forceinline__ void scan_chunk(const Args &a, int row, int chunk, un
             for (int e = 0; e < VW; ++e) {
                 const float xv = x[v * VW + e];
                 if (xv >= thr) {
-                    if (pos < cap) {
-                        Cand cd;
-                        cd.y = xv;
-                        cd.idx = c0 + li + e;
-                        out[pos] = cd;
-                    }
+                    // past the capacity the last slot is overwritten: an overflowed
+                    // chunk's candidates are never read (its row takes the full-row path)
+                    Cand cd;
+                    cd.y = xv;
+                    cd.idx = c0 + li + e;
+                    out[(unsigned)min(pos, cap - 1)] = cd;
                     ++pos;
                 }
             }
