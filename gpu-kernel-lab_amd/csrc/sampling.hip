@@ -301,6 +301,10 @@ template <typename TIn> struct Loader;
 // The streaming pass reads every logit once: its 16-byte loads are non-temporal.
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+// Fourth word of a raw buffer resource on gfx9-family GPUs (32-bit data format, no
+// swizzle); the third word is the range in bytes, stores beyond it are dropped.
+constexpr int kBufferRsrcWord3 = 0x00020000;
 template <> struct Loader<float> {
     static constexpr int VW = 4;
     __device__ static __forceinline__ void vec(const float *p, float *o) {
@@ -2821,8 +2825,11 @@ __device__ __forceinline__ void scan_chunk(const Args &a, int row, int chunk, un
         const int total = ms.ncand;
         // scores are written as streamed: top-k rows in the penalised space (the row
         // kernel divides by T), the others in final space
+        // the chunk's slots as a buffer resource: stores past the capacity are dropped by
+        // the hardware's range check (an overflowed chunk's slots are never read anyway)
         Cand *out = a.cands + ((size_t)row * a.S + chunk) * a.cand_cap;
-        const int cap = a.cand_cap;
+        const __amdgpu_buffer_rsrc_t slots =
+            __builtin_amdgcn_make_buffer_rsrc(out, (short)0, a.cand_cap * (int)sizeof(Cand), kBufferRsrcWord3);
 #pragma unroll
         for (int v = 0; v < NV; ++v) {
             const int li = (v * kThreads + tid) * VW;
@@ -2830,18 +2837,14 @@ __device__ __forceinline__ void scan_chunk(const Args &a, int row, int chunk, un
             for (int e = 0; e < VW; ++e) {
                 const float xv = x[v * VW + e];
                 if (xv >= thr) {
-                    // past the capacity the last slot is overwritten: an overflowed
-                    // chunk's candidates are never read (its row takes the full-row path)
-                    Cand cd;
-                    cd.y = xv;
-                    cd.idx = c0 + li + e;
-                    out[(unsigned)min(pos, cap - 1)] = cd;
+                    const u32x2 cd = {__float_as_uint(xv), (uint32_t)(c0 + li + e)};
+                    __builtin_amdgcn_raw_buffer_store_b64(cd, slots, (uint32_t)pos * (uint32_t)sizeof(Cand), 0, 0);
                     ++pos;
                 }
             }
         }
-        st.ncand = min(total, cap);
-        st.overflow = total > cap ? 1 : 0;
+        st.ncand = min(total, a.cand_cap);
+        st.overflow = total > a.cand_cap ? 1 : 0;
     } else {
         __syncthreads();
     }
