@@ -305,11 +305,18 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 // Fourth word of a raw buffer resource on gfx9-family GPUs (32-bit data format, no
 // swizzle); the third word is the range in bytes, stores beyond it are dropped.
 constexpr int kBufferRsrcWord3 = 0x00020000;
+constexpr int kBufferNonTemporal = 2;   // cache-policy operand of buffer loads: nt
+// vec_rsrc (fp32): the same from a buffer resource at byte offset voff + soff (soff
+// uniform), non-temporal; positions past the resource's range read 0.
 template <> struct Loader<float> {
     static constexpr int VW = 4;
     __device__ static __forceinline__ void vec(const float *p, float *o) {
         const f32x4 v = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(p));
         o[0] = v.x; o[1] = v.y; o[2] = v.z; o[3] = v.w;
+    }
+    __device__ static __forceinline__ void vec_rsrc(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff, float *o) {
+        const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, kBufferNonTemporal);
+        o[0] = __uint_as_float(v.x); o[1] = __uint_as_float(v.y); o[2] = __uint_as_float(v.z); o[3] = __uint_as_float(v.w);
     }
     __device__ static __forceinline__ float one(const float *p) { return *p; }
 };
@@ -323,6 +330,7 @@ template <> struct Loader<uint16_t> {
         o[4] = bf(v.z & 0xffffu); o[5] = bf(v.z >> 16);
         o[6] = bf(v.w & 0xffffu); o[7] = bf(v.w >> 16);
     }
+
     __device__ static __forceinline__ float one(const uint16_t *p) { return bf(*p); }
 };
 
@@ -2616,17 +2624,31 @@ __device__ __forceinline__ void scan_chunk(const Args &a, int row, int chunk, un
 
     // Rows that cannot take 16-byte loads (unaligned, or a last chunk shorter than one
     // vector) run the kVec = false instantiation.  Otherwise every chunk takes the same
-    // vector loads, with addresses clamped to the last whole vector of a partial chunk
-    // (a no-op for full ones): one load path, so the history count below waits for the
-    // ids only, with the logits still in flight.  Positions past cn are masked after the
-    // count; the vector straddling cn (if any) is re-read element by element (every
-    // thread of a partial chunk reads it, its owner keeps it).
+    // vector loads (fp32: through a buffer resource over the chunk, 32-bit offsets,
+    // vectors past its end reading 0; bf16: addresses clamped to the last whole vector of
+    // a partial chunk, which keeps its registers within budget): one load path, so the
+    // history count below waits for the ids only, with the logits still in flight.
+    // Positions past cn are masked after the count; the vector straddling cn (if any) is
+    // re-read element by element (every thread of a partial chunk reads it, its owner
+    // keeps it).
     float x[E];
     float ptail[VW];
     if (kVec) {
-        const int lastfull = (cn / VW - 1) * VW;
+        // the chunk as a buffer resource: 32-bit offsets (one per thread, the vector's
+        // stride uniform), and vectors past the chunk's end read 0 instead of being
+        // clamped (they are masked below)
+        if constexpr (sizeof(TIn) == 4) {
+            const __amdgpu_buffer_rsrc_t lg = __builtin_amdgcn_make_buffer_rsrc(
+                const_cast<TIn *>(src), (short)0, cn * (int)sizeof(TIn), kBufferRsrcWord3);
+            const uint32_t vo = (uint32_t)tid * (uint32_t)(VW * sizeof(TIn));
 #pragma unroll
-        for (int v = 0; v < NV; ++v) Loader<TIn>::vec(src + min((v * kThreads + tid) * VW, lastfull), &x[v * VW]);
+            for (int v = 0; v < NV; ++v)
+                Loader<TIn>::vec_rsrc(lg, vo, (uint32_t)(v * kThreads * VW * sizeof(TIn)), &x[v * VW]);
+        } else {
+            const int lastfull = (cn / VW - 1) * VW;
+#pragma unroll
+            for (int v = 0; v < NV; ++v) Loader<TIn>::vec(src + min((v * kThreads + tid) * VW, lastfull), &x[v * VW]);
+        }
         if (cn < C) {
             const int ls = (cn / VW) * VW;
 #pragma unroll
