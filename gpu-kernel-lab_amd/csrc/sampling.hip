@@ -2208,8 +2208,9 @@ __device__ __forceinline__ bool combine_row(const Args &a, int row, const klsamp
             }
         }
     }
-    arg = wave_reduce(arg, OpMinI(), 0x7fffffff);
-    Z = wave_reduce(Z, OpSumD(), 0.0);
+    // (the argmax serves greedy rows only, the sum-exp all but top-k rows)
+    if (mode == kGreedy) arg = wave_reduce(arg, OpMinI(), 0x7fffffff);
+    if (mode != kTopK) Z = wave_reduce(Z, OpSumD(), 0.0);
     kmin = wave_reduce(kmin, OpMinU(), 0xffffffffu);
     kmax = wave_reduce(kmax, OpMaxU(), 0u);
     if (lane_id() == 0) {
