@@ -2228,14 +2228,57 @@ __device__ __forceinline__ bool combine_row(const Args &a, int row, const klsamp
     float ylo = fkey_inv(ms.kmin), yhi = fkey_inv(ms.kmax);
     const bool narrowed = nF > kSortCap;   // the radix narrowing below leaves ms.hist used
     if (nF > kSortCap) {
-        // too many candidates for LDS: narrow them to the best R with a radix select over
-        // the candidate slots
+        // Too many candidates for LDS: narrow them to the best R.  First a 256-bin
+        // histogram over [ylo, yhi] (two passes over the candidate slots): the entries in
+        // the bins at or above the R-th's, if they fit; else a radix select over the slots
+        // (four passes) for the R-th and the entries scoring at least it.
         const int R = (mode == kTopK) ? p.top_k : (mode == kTopP ? kThreads : N);
         if (R < 1 || R > kSortCap) return false;
         const CandSource src{rc, cnt, S, a.cand_cap, xs};
-        ylo = fkey_inv(select_kth(src, (uint32_t)R, ms));
-        nF = gather_keys(src, ylo, A, kSortCap, ms);
-        if (nF > kSortCap) return false;
+        const float span = yhi - ylo, scale = 256.f / span;
+        int t = -1;
+        if (span > 0.f && scale <= __FLT_MAX__) {
+            auto bin = [&](float y) { return min(255, (int)((y - ylo) * scale)); };
+            ms.hist[tid] = 0u;   // kThreads == 256 bins
+            __syncthreads();     // (every wave has read the candidate count)
+            if (tid == 0) ms.ncand = 0;
+            src.each([&](uint32_t, int, float y) { atomicAdd(&ms.hist[bin(y)], 1u); });
+            __syncthreads();
+            // the R-th from the top: every wave finds its bin from the same histogram
+            const int l = lane_id();
+            uint32_t c[4], sum = 0u;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) { c[j] = ms.hist[255 - 4 * l - j]; sum += c[j]; }
+            const uint32_t incl = wave_incl_scan(sum);
+            const unsigned long long reach = __ballot(incl >= (uint32_t)R);
+            const int fl = reach ? __ffsll((long long)reach) - 1 : 63;
+            int b = 0;
+            if (l == fl) {
+                uint32_t acc = incl - sum;
+                b = 252 - 4 * l;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    if (acc + c[j] >= (uint32_t)R) { b = 255 - 4 * l - j; break; }
+                    acc += c[j];
+                }
+            }
+            b = __builtin_amdgcn_readlane(b, fl);
+            src.each([&](uint32_t, int idx, float y) {
+                if (bin(y) >= b) {
+                    const int pos = wave_append(&ms.ncand);
+                    if (pos < kSortCap) A[pos] = desc_key(y, idx);
+                }
+            });
+            __syncthreads();
+            t = ms.ncand;
+        }
+        if (t >= R && t <= kSortCap) {
+            nF = t;
+        } else {
+            ylo = fkey_inv(select_kth(src, (uint32_t)R, ms));
+            nF = gather_keys(src, ylo, A, kSortCap, ms);
+            if (nF > kSortCap) return false;
+        }
     }
     // D[0..n) := the best R of F (ties with the R-th included), sorted best first
     auto best = [&](int R) -> int {
