@@ -2380,6 +2380,7 @@ __device__ __forceinline__ bool combine_row(const Args &a, int row, const klsamp
                 wave_finish(a, row, mode, p, Es, lk, L, mref, A, ms.irank, true, wz);
             }
         };
+        int lk_pre = -1;   // the top set is D[0..lk_pre), sorted by score (set below)
         if (nF > kk && N <= 64) {
             // one histogram pass isolates the kk best; sorted, they give the kk-th
             // quotient, and the top set (every candidate whose quotient reaches it) is
@@ -2437,6 +2438,7 @@ __device__ __forceinline__ bool combine_row(const Args &a, int row, const klsamp
             if (t >= kk && t <= 256) {
                 block_rank_sort(D, t, ms.part);
                 const float xt = quotient_threshold(__fdiv_rn(desc_key_y(D[kk - 1]), p.temperature), p.temperature);
+                const float xlast = desc_key_y(D[t - 1]);   // (read before D may be rewritten)
                 unsigned long long *Et = D + 256;
                 for (int i = tid; i < nF; i += kThreads) {
                     const unsigned long long k = A[i];
@@ -2462,21 +2464,31 @@ __device__ __forceinline__ bool combine_row(const Args &a, int row, const klsamp
                     finish_top(Es, lk);
                     return true;
                 }
+                // more than 64 reach the k-th quotient: when every candidate reaching it
+                // is in the sorted gather (its threshold is no lower than the gather's
+                // smallest score), the top set is the gather's first lk entries
+                if (xt >= xlast && lk <= t) lk_pre = lk;
             }
         }
-        float xt = kNegInf;
-        if (nF > kk) {
-            if (best(kk) < 0) return false;
-            xt = quotient_threshold(__fdiv_rn(desc_key_y(D[kk - 1]), p.temperature), p.temperature);
+        int lk = lk_pre;
+        if (lk < 0) {
+            float xt = kNegInf;
+            if (nF > kk) {
+                if (best(kk) < 0) return false;
+                xt = quotient_threshold(__fdiv_rn(desc_key_y(D[kk - 1]), p.temperature), p.temperature);
+            }
+            lk = gather_ge(A, nF, xt, D, kSortCap, ms);
+            if (lk > kSortCap) return false;
         }
-        const int lk = gather_ge(A, nF, xt, D, kSortCap, ms);
-        if (lk > kSortCap) return false;
-        for (int i = tid; i < lk; i += kThreads) {
-            const unsigned long long k = D[i];
-            D[i] = desc_key(__fdiv_rn(desc_key_y(k), p.temperature), desc_key_idx(k));
+        if (lk_pre < 0 || p.temperature != 1.f) {
+            // divided and sorted in final space (a gather already sorted at T = 1 stays)
+            for (int i = tid; i < lk; i += kThreads) {
+                const unsigned long long k = D[i];
+                D[i] = desc_key(__fdiv_rn(desc_key_y(k), p.temperature), desc_key_idx(k));
+            }
+            __syncthreads();
+            sort_top(D, lk, ms);
         }
-        __syncthreads();
-        sort_top(D, lk, ms);
         const double mref = (double)desc_key_y(D[0]);
         const bool topp = (p.flags & KLSAMPLE_ROW_TOP_P) != 0;
         if (lk <= 64 && N <= 64) {
