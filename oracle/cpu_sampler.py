@@ -57,6 +57,9 @@ class OracleRow:
     topp_exact_kept: int | None = None     # kept count of the exact (float64) top-p cut
     topp_exact_margin: float = math.inf    # |exact excl - p| nearest the exact cut
     cdf_margin: float = math.inf           # |cdf step - u*Z| / Z nearest the token
+    # the final log-softmax in exact arithmetic (float64 over the same fp32 final scores)
+    exact_logprob: float = math.nan        # of the token
+    lse_error: float = 0.0                 # |the reference's fp32 log-normaliser - the exact one|
     notes: list = field(default_factory=list)
 
     @property
@@ -164,6 +167,8 @@ def restated_sample(logits: torch.Tensor, history=(), params=None, *, u: float |
         (int(i), float(v)) for v, i in zip(*log_probabilities.topk(count)))
     row.token_id = token
     row.logprob = float(log_probabilities[token])                  # :63
+    if diagnostics:
+        _lse_diagnostics(row, scores, token)
     row.top_logprobs = top
     row.stopped = token in p.stop_token_ids
     row.scores = scores
@@ -198,6 +203,21 @@ def _topp_diagnostics(row: OracleRow, ordered, excl, remove, top_p, total: float
         cut = row.topp_exact_kept
         em = [abs(ex[j] - p32) for j in (cut - 1, cut) if 0 <= j < n and w[j] > 0]
         row.topp_exact_margin = min(em) if em else math.inf
+
+
+def _lse_diagnostics(row: OracleRow, scores, token: int) -> None:
+    """The token's log-softmax in float64 over the final fp32 scores, and how far the
+    reference's fp32 log-normaliser (``scores[token] - logprob``) lies from the exact
+    one: over ~10^5 entries its fp32 sum carries a relative error of ~1e-5."""
+    s = scores.double().numpy()
+    fin = np.isfinite(s)
+    if not fin.any() or not np.isfinite(s[token]):
+        return
+    m = s[fin].max()
+    lse = m + math.log(np.exp(s[fin] - m).sum())
+    row.exact_logprob = float(s[token] - lse)
+    if math.isfinite(row.logprob):
+        row.lse_error = abs((float(s[token]) - row.logprob) - lse)
 
 
 def _cdf_diagnostics(row: OracleRow, probs, token: int, u: float) -> None:

@@ -168,6 +168,25 @@ def test_logprob_is_log_softmax_of_final_scores():
     assert greedy.logprob == pytest.approx(x.max() - lse_all, abs=2e-6)
 
 
+def test_exact_log_normaliser_closed_forms():
+    # equal scores: every logprob is -log(n) exactly; the reference's fp32 value is close
+    flat = restated_sample(torch.zeros(100_000), (), P(logprobs=1))
+    assert flat.exact_logprob == pytest.approx(-math.log(100_000), abs=1e-12)
+    assert flat.lse_error == pytest.approx(abs(-flat.logprob - math.log(100_000)), abs=1e-12)
+    assert flat.lse_error < 1e-4
+    # two values a > b, n_b copies of b: log(1 / (1 + n_b e^(b - a))) at the argmax
+    x = torch.full((50_001,), -3.0)
+    x[7] = 4.0
+    two = restated_sample(x, (), P(logprobs=1))
+    assert two.token_id == 7
+    assert two.exact_logprob == pytest.approx(-math.log1p(50_000 * math.exp(-7.0)), abs=1e-12)
+    # masked entries take no part; a masked-out token has no exact value
+    y = torch.tensor([1.0, 2.0, -math.inf, 0.5])
+    r = restated_sample(y, (), P(temperature=1.0), u=0.0)
+    assert r.token_id == 0
+    assert r.exact_logprob == pytest.approx(1.0 - math.log(math.e + math.e ** 2 + math.e ** 0.5), abs=1e-12)
+
+
 def test_greedy_takes_lowest_index_of_ties():
     assert restated_sample(torch.tensor([1., 5., 2., 5.]), (), P()).token_id == 1
     assert restated_sample(torch.tensor([-1., -1., -1.]), (), P()).token_id == 0

@@ -339,3 +339,57 @@ def test_other_chunk_sizes(elems, monkeypatch):
         rows = sample_rows(w.logits, w.histories, w.params, w.uniforms)
         out = run(w.logits, w.params, w.histories, w.uniforms, probs=True)
         check(out, rows, w.params, probs=True)
+
+
+# ---- randomised configurations -----------------------------------------------------------
+
+
+def _random_case(seed):
+    """A seeded batch mixing vocab sizes, dtypes, score shapes (wide, heavy head, value
+    ties on a 0.5 grid, mostly masked, nearly flat), every mode and penalty, histories
+    with heavy repeats, and the full-row path."""
+    rng = np.random.default_rng(seed)
+    V = int(rng.choice([rng.integers(1, 300), rng.integers(300, 20000), rng.integers(20000, 160000), 151936]))
+    B = int(rng.integers(1, 33)) if V <= 60000 else int(rng.integers(1, 13))
+    dtype = torch.bfloat16 if rng.random() < 0.5 else torch.float32
+    shape = str(rng.choice(['wide', 'heavy', 'ties', 'masked', 'flat']))
+    x = rng.standard_normal((B, V)).astype(np.float32) * float(rng.uniform(0.3, 8.0))
+    if shape == 'heavy':
+        for b in range(B):
+            x[b, rng.integers(0, V, size=min(V, int(rng.integers(1, 40))))] += rng.uniform(5, 25)
+    elif shape == 'ties':
+        x = np.round(x * 2) / 2
+    elif shape == 'masked':
+        x[rng.random((B, V)) < rng.uniform(0.1, 0.95)] = -np.inf
+        x[:, 0] = np.maximum(x[:, 0], 0)
+    elif shape == 'flat':
+        x *= 0.01
+    params, hist = [], []
+    for _ in range(B):
+        T = 0.0 if rng.random() < 0.2 else float(rng.choice([1.0, rng.uniform(0.2, 2.5)]))
+        k = 0 if rng.random() < 0.4 else int(rng.choice([rng.integers(1, 64), rng.integers(64, 3000),
+                                                         rng.integers(1, V + 5)]))
+        p = 1.0 if rng.random() < 0.35 else float(rng.choice([rng.uniform(0.05, 0.999), rng.uniform(0.9, 0.9999)]))
+        params.append(SamplingParams(
+            temperature=T, top_k=k, top_p=p,
+            repetition_penalty=1.0 if rng.random() < 0.4 else float(rng.uniform(0.7, 1.6)),
+            logprobs=int(rng.choice([0, 1, 4, 20, rng.integers(0, 65)])),
+            presence_penalty=0.0 if rng.random() < 0.5 else float(rng.uniform(-0.5, 1.0)),
+            frequency_penalty=0.0 if rng.random() < 0.5 else float(rng.uniform(-0.3, 0.8))))
+        n = int(rng.choice([0, rng.integers(0, 100), rng.integers(0, 3000)]))
+        hist.append(rng.integers(0, min(V, 20) if rng.random() < 0.2 else V, n).tolist())
+    u = rng.random(B).astype(np.float32)
+    options = _lib.OPT_FORCE_DENSE if rng.random() < 0.15 else 0
+    return torch.from_numpy(x).to(dtype), params, hist, u, options, shape
+
+
+@pytest.mark.parametrize('block', range(6))
+def test_randomised_configurations(block):
+    """Forty seeded random batches per block against the oracle, with probabilities
+    on every third."""
+    for seed in range(40 * block, 40 * block + 40):
+        logits, params, hist, u, options, shape = _random_case(90_000 + seed)
+        say(f'random seed={90_000 + seed} shape={shape}')
+        rows = sample_rows(logits, hist, params, u)
+        out = run(logits, params, hist, u, options=options, probs=seed % 3 == 0)
+        check(out, rows, params, probs=seed % 3 == 0)
