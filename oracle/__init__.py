@@ -3,8 +3,8 @@
 TEST INFRASTRUCTURE ONLY. Nothing in the product (the ``klsample`` package, its HIP
 library or its C ABI) imports, links or calls this package. Only ``tests/``,
 ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of ``bench.py`` use it, and
-there only as the checker (or as the timed CPU baseline), never as the path measured
-or shipped.
+there only to check results (or as the timed CPU baseline), never as the path
+measured or shipped.
 
 ``oracle.cpu_sampler`` restates the reference sampler (``serving/sampling.py:44-63``)
 with the same PyTorch CPU operations, in two modes:

@@ -98,8 +98,8 @@ def test_engine_style_loop_runs_unchanged():
 
 
 def test_integration_ctypes_stub_matches_the_drop_in():
-    """The raw ctypes binding shown in INTEGRATION.md runs as written and returns the
-    drop-in's tokens and logprobs."""
+    """The raw ctypes binding printed in the repository's integration guide runs as
+    written and returns the drop-in's tokens and logprobs."""
     import re
     from pathlib import Path
 
@@ -111,7 +111,7 @@ def test_integration_ctypes_stub_matches_the_drop_in():
     stub = next(b for b in blocks if 'klsample_run' in b)
     stub = stub.replace('/path/to/repo/gpu-kernel-lab_amd/klsample/libklsample.so', str(_lib.LIBRARY))
     ns = {}
-    exec(compile(stub, 'INTEGRATION.md', 'exec'), ns)
+    exec(compile(stub, '<integration stub>', 'exec'), ns)
     w = workloads.make('cpu_reference_b8', num_logprobs=3)
     hist = [[5, 9, -1]] * w.batch
     params = [SamplingParams(p.temperature, p.top_k, p.top_p, 1.2, p.stop_token_ids, p.seed, 3) for p in w.params]
