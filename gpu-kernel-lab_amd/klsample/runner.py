@@ -154,6 +154,13 @@ class DeviceRunner:
         if logits.dtype not in _DTYPES:
             logits = logits.float()
         B, V = logits.shape
+        # the kernels read one parameter record, CSR offset pair and uniform per logits row
+        if len(params_list) != B:
+            raise ValueError(f'one SamplingParams per row is required ({len(params_list)} for {B} rows)')
+        if histories is not None and len(histories) != B:
+            raise ValueError(f'one history per row is required ({len(histories)} for {B} rows)')
+        if uniforms is not None and len(uniforms) != B:
+            raise ValueError(f'one uniform per row is required ({len(uniforms)} for {B} rows)')
         # rows must not overlap (a size-1 dimension may carry any stride)
         if logits.stride(1) != 1 or (B > 1 and logits.stride(0) < V):
             logits = logits.contiguous()

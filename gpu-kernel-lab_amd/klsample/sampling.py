@@ -103,12 +103,14 @@ class Sampler:
         sampled row consumes one uniform of its own request's generator, so results
         equal B separate ``sample`` calls."""
         if isinstance(logits, torch.Tensor) and logits.dim() == 2:
-            rows, devices = logits, [logits.device] * len(samplers)
+            rows, devices = logits, [logits.device] * logits.shape[0]
         else:
             rows = list(logits)
             devices = [r.device for r in rows]
         if len(devices) != len(samplers):
             raise ValueError('one sampler per row is required')
+        if histories is not None and len(histories) != len(samplers):
+            raise ValueError('one history per row is required')
         params = [s.params for s in samplers]
         us = [s.next_uniform(d) if s.params.temperature != 0 else 0.0 for s, d in zip(samplers, devices)]
         return _run(rows, params, histories, us)

@@ -11,11 +11,18 @@ so that on the same fp32 inputs it produces the same scores bit for bit, and add
   after the repetition penalty over the same history;
 * ``uniform`` mode, where the multinomial draw (``serving/sampling.py:60``) becomes
   an inverse CDF on a caller-supplied uniform ``u``;
-* per-row diagnostics that classify a row as a *boundary row* (the top-p crossing,
-  a value tie or the CDF step lies within ``1e-6`` of the cut), which is the only
-  class of row whose token id may differ from a GPU implementation;
+* per-row diagnostics that classify a row as a *boundary row* (the top-p crossing or
+  the CDF step lies within ``1e-6`` of the cut), which is the only class of row whose
+  token id may differ from a GPU implementation;
 * an exact evaluation of the top-p cut (float64 weights and cumulative sum over the
-  same sorted order).  The reference's fp32 ``softmax`` over a 151,936-entry row sums
+  same sorted order);
+* ``stable`` tie order: the reference sorts with an unstable ``sort``
+  (``serving/sampling.py:57``) and takes its top-N with ``topk`` (``:62``), so which of
+  several equal scores is kept at the top-p cut, and the order of equal top-N entries,
+  are implementation-defined there.  With ``stable=True`` equal scores are taken in
+  ascending index order in both places, and top-N slots past the kept set list the
+  smallest ids whose final score is ``-inf``.  The kept *count*, every probability and
+  every logprob are the reference's; only the identities among equal scores are fixed.  The reference's fp32 ``softmax`` over a 151,936-entry row sums
   to ``1 + delta`` with ``|delta|`` up to ~3e-5 (measured: the last element of its own
   ``cumsum``), so its cut can differ from the exact one by a few tokens; the top-p
   boundary band is therefore ``1e-6 + |delta|`` wide, and implementations are also
@@ -50,6 +57,9 @@ class OracleRow:
     probs: torch.Tensor | None = None      # vector handed to the draw (sampled rows)
     scores: torch.Tensor | None = None     # final scores (after penalties, T, top-k/p)
     kept: int = 0                          # number of finite final scores
+    exact_probs: np.ndarray | None = None  # float64 softmax of the final scores (sampled rows)
+    pre_topp: torch.Tensor | None = None   # scores entering the top-p step (top_p < 1 rows)
+    topp_exact_cut: tuple | None = None    # (score, index) of the last entry the exact cut keeps
     # boundary classification (sampled rows only)
     topp_margin: float = math.inf          # |excl_cumsum - p| nearest the cut (reference arithmetic)
     topp_norm_error: float = 0.0           # |sum of the reference's top-p probabilities - 1|
@@ -63,9 +73,33 @@ class OracleRow:
     notes: list = field(default_factory=list)
 
     @property
+    def margin_row(self) -> bool:
+        """The top-p decision lies within 1e-6 of p, widened by the reference's own fp32
+        normalisation error ``delta``: its cut may then fall one entry away from the
+        exact (float64) cut."""
+        return self.topp_margin < BOUNDARY_EPS + self.topp_norm_error
+
+    @property
+    def cdf_row(self) -> bool:
+        """``u * Z`` lies within 1e-6 (relative) of a CDF step next to the token."""
+        return self.cdf_margin < BOUNDARY_EPS
+
+    @property
     def boundary(self) -> bool:
-        return (self.topp_margin < BOUNDARY_EPS + self.topp_norm_error or self.topp_tie
-                or self.cdf_margin < BOUNDARY_EPS)
+        """A row whose token id may differ from an implementation's: a top-p mass margin
+        or a CDF-step margin.  A value tie across the cut is not one: with ``stable`` tie
+        order the kept identities are fixed (ascending index)."""
+        return self.margin_row or self.cdf_row
+
+    def in_kept(self, token: int) -> bool:
+        """Whether ``token`` is kept by this row's final scores or by the exact top-p cut."""
+        if self.scores is not None and math.isfinite(float(self.scores[token])):
+            return True
+        if self.pre_topp is None or self.topp_exact_cut is None:
+            return False
+        s = float(self.pre_topp[token])
+        cs, ci = self.topp_exact_cut
+        return s > cs or (s == cs and token <= ci)
 
 
 def normalize_history(history, vocab: int) -> np.ndarray:
@@ -122,11 +156,13 @@ def _apply_penalties(scores: torch.Tensor, ids: np.ndarray, params) -> None:
 
 
 def restated_sample(logits: torch.Tensor, history=(), params=None, *, u: float | None = None,
-                    generator: torch.Generator | None = None, diagnostics: bool = True) -> OracleRow:
+                    generator: torch.Generator | None = None, diagnostics: bool = True,
+                    stable: bool = False) -> OracleRow:
     """One reference ``Sampler.sample`` call (``serving/sampling.py:44-63``).
 
     ``u`` selects uniform mode (inverse CDF); otherwise ``generator`` drives
-    ``torch.multinomial`` exactly as the reference does.
+    ``torch.multinomial`` exactly as the reference does.  ``stable`` fixes the order of
+    equal scores (ascending index) in the top-p sort and the top-N list.
     """
     if logits.ndim != 1 or not logits.is_floating_point():        # :45
         raise ValueError('logits must be a floating vector')
@@ -145,13 +181,15 @@ def restated_sample(logits: torch.Tensor, history=(), params=None, *, u: float |
             cutoff = scores.topk(k).values[-1]
             scores.masked_fill_(scores < cutoff, -torch.inf)
         if p.top_p < 1:                                            # :56-59
-            ordered, index = scores.sort(descending=True)
+            if diagnostics:
+                row.pre_topp = scores.clone()
+            ordered, index = scores.sort(descending=True, stable=stable)
             probabilities = ordered.softmax(0)
             cumulative = probabilities.cumsum(0)
             excl = cumulative - probabilities
             remove = excl > p.top_p
             if diagnostics:
-                _topp_diagnostics(row, ordered, excl, remove, p.top_p, float(cumulative[-1]))
+                _topp_diagnostics(row, ordered, index, excl, remove, p.top_p, float(cumulative[-1]))
             scores[index[remove]] = -torch.inf
         probs = scores.softmax(0)                                  # :60
         row.probs = probs
@@ -163,12 +201,28 @@ def restated_sample(logits: torch.Tensor, history=(), params=None, *, u: float |
             token = int(torch.multinomial(probs, 1, generator=generator))
     log_probabilities = scores.log_softmax(0)                      # :61
     count = min(p.logprobs, vocab)
-    top = () if not count else tuple(                              # :62
-        (int(i), float(v)) for v, i in zip(*log_probabilities.topk(count)))
+    if not count:
+        top = ()
+    elif stable:
+        # equal values in index order; past the kept set the -inf entries in index order
+        # are the smallest ids not listed before them
+        v, i = log_probabilities.sort(descending=True, stable=True)
+        top = tuple((int(a), float(b)) for b, a in zip(v[:count], i[:count]))
+    else:
+        top = tuple((int(i), float(v)) for v, i in zip(*log_probabilities.topk(count)))   # :62
     row.token_id = token
     row.logprob = float(log_probabilities[token])                  # :63
     if diagnostics:
         _lse_diagnostics(row, scores, token)
+        if p.temperature != 0:
+            s = scores.double().numpy()
+            fin = np.isfinite(s)
+            ep = np.zeros_like(s)
+            if fin.any():
+                m = s[fin].max()
+                e = np.exp(s[fin] - m)
+                ep[fin] = e / e.sum()
+            row.exact_probs = ep
     row.top_logprobs = top
     row.stopped = token in p.stop_token_ids
     row.scores = scores
@@ -176,7 +230,7 @@ def restated_sample(logits: torch.Tensor, history=(), params=None, *, u: float |
     return row
 
 
-def _topp_diagnostics(row: OracleRow, ordered, excl, remove, top_p, total: float) -> None:
+def _topp_diagnostics(row: OracleRow, ordered, index, excl, remove, top_p, total: float) -> None:
     """Distance of the top-p decision from its cut, the reference's normalisation
     error, ties across the cut, and the exact (float64) cut over the same order."""
     p32 = float(np.float32(top_p))            # torch compares against fp32(top_p)
@@ -201,6 +255,8 @@ def _topp_diagnostics(row: OracleRow, ordered, excl, remove, top_p, total: float
         keep = ex <= p32
         row.topp_exact_kept = int(keep.sum())
         cut = row.topp_exact_kept
+        if cut > 0:
+            row.topp_exact_cut = (float(o[cut - 1]), int(index[cut - 1]))
         em = [abs(ex[j] - p32) for j in (cut - 1, cut) if 0 <= j < n and w[j] > 0]
         row.topp_exact_margin = min(em) if em else math.inf
 
@@ -232,13 +288,15 @@ def _cdf_diagnostics(row: OracleRow, probs, token: int, u: float) -> None:
 
 
 def sample_rows(logits2d: torch.Tensor, histories, params_list, uniforms=None,
-                generators=None, diagnostics: bool = True) -> list[OracleRow]:
+                generators=None, diagnostics: bool = True, stable: bool = True) -> list[OracleRow]:
     """Row loop over a ``[B, V]`` batch, one reference call per row (as
-    ``serving/engine.py:92-96`` calls the sampler once per request row)."""
+    ``serving/engine.py:92-96`` calls the sampler once per request row).  Parity uses
+    the stable tie order by default (see ``restated_sample``)."""
     out = []
     for b in range(logits2d.shape[0]):
         u = None if uniforms is None else float(uniforms[b])
         g = None if generators is None else generators[b]
         out.append(restated_sample(logits2d[b], histories[b] if histories is not None else (),
-                                   params_list[b], u=u, generator=g, diagnostics=diagnostics))
+                                   params_list[b], u=u, generator=g, diagnostics=diagnostics,
+                                   stable=stable))
     return out

@@ -89,6 +89,32 @@ def test_sampler_rejects_bad_logits():
         s.sample(torch.tensor([1, 2, 3]))
 
 
+def test_sample_many_rejects_row_count_mismatches_before_drawing():
+    """A padded [B, V] decode batch with fewer samplers (or histories) than rows is an
+    error, raised before any uniform is drawn or any launch is made."""
+    s = [Sampler(SamplingParams(temperature=1.0, seed=5)) for _ in range(2)]
+    with pytest.raises(ValueError):
+        Sampler.sample_many(s, torch.zeros(3, 10), [(), ()])
+    with pytest.raises(ValueError):
+        Sampler.sample_many(s, torch.zeros(2, 10), [(), (), ()])
+    with pytest.raises(ValueError):
+        Sampler.sample_many(s, [torch.zeros(10)], [()])
+    fresh = Sampler(SamplingParams(temperature=1.0, seed=5))
+    assert s[0].next_uniform('cpu') == fresh.next_uniform('cpu')   # no uniform was consumed
+
+
+def test_device_runner_checks_rows_before_staging():
+    from klsample.runner import DeviceRunner
+    r = DeviceRunner.__new__(DeviceRunner)   # no device needed: the checks come first
+    x = torch.zeros(3, 10)
+    with pytest.raises(ValueError):
+        r.run(x, [SamplingParams()] * 2, None, None, 0)
+    with pytest.raises(ValueError):
+        r.run(x, [SamplingParams()] * 3, [()] * 2, None, 0)
+    with pytest.raises(ValueError):
+        r.run(x, [SamplingParams()] * 3, None, [0.5] * 4, 0)
+
+
 def test_uniform_stream_is_per_request_and_seeded():
     a, b = Sampler(SamplingParams(temperature=1.0, seed=3)), Sampler(SamplingParams(temperature=1.0, seed=3))
     ua = [a.next_uniform('cpu') for _ in range(4)]

@@ -226,9 +226,22 @@ def test_history_normalisation_matches_indexing():
 
 
 def test_boundary_classification():
-    # exact value tie straddling the top-p cut
-    row = restated_sample(torch.tensor([2., 1., 1., 0.]), (), P(temperature=1.0, top_p=0.7), u=0.5)
-    assert row.topp_tie and row.boundary
+    # an exact value tie straddling the top-p cut is flagged, but it is no boundary row:
+    # the stable order keeps the lower index
+    row = restated_sample(torch.tensor([2., 1., 1., 0.]), (), P(temperature=1.0, top_p=0.73), u=0.99, stable=True)
+    assert row.topp_tie and not row.boundary
+    assert torch.isfinite(row.scores).tolist() == [True, True, False, False]
+    # the top-p mass at the cut within 1e-6 of p: a margin row
+    w = np.array([0.5, 0.3, 0.2])
+    x = torch.from_numpy(np.log(w).astype(np.float32))
+    xd = x.double().numpy()
+    mass = float(np.exp(xd[0]) / np.exp(xd).sum())
+    row = restated_sample(x, (), P(temperature=1.0, top_p=mass + 2e-7), u=0.3, stable=True)
+    assert row.margin_row and row.boundary
+    # u * Z within 1e-6 of a CDF step
+    full = restated_sample(x, (), P(temperature=1.0), u=0.3, stable=True)
+    row = restated_sample(x, (), P(temperature=1.0), u=float(full.probs[0]) + 1e-7, stable=True)
+    assert row.cdf_row and row.boundary and not row.margin_row
     # far from every cut
     row = restated_sample(torch.tensor([3., 1., 0.5, 0.]), (), P(temperature=1.0, top_p=0.5), u=0.2)
     assert not row.boundary
@@ -249,3 +262,124 @@ def test_sample_rows_loops_rows():
     x = torch.tensor([[0., 1., 3., 2.], [3., 2., 1., 0.]])
     rows = sample_rows(x, [[2], []], [P(repetition_penalty=1.1), P()], None)
     assert [r.token_id for r in rows] == [2, 0]
+
+
+# ---- the stable tie order and the parity checker itself ----------------------------------
+
+def test_stable_tie_order_keeps_the_reference_count_and_lowest_indices():
+    """Stable order changes only which of equal scores are kept at the top-p cut: the
+    kept count, every probability and logprob stay the reference's."""
+    rng = np.random.default_rng(31)
+    for trial in range(40):
+        v = int(rng.integers(5, 400))
+        x = torch.from_numpy((np.round(rng.standard_normal(v) * 2) / 2).astype(np.float32))  # many ties
+        params = P(temperature=float(rng.uniform(0.5, 1.5)), top_k=int(rng.choice([0, 10, 50])),
+                   top_p=float(rng.uniform(0.3, 0.99)), logprobs=8)
+        u = float(rng.random())
+        ref = restated_sample(x, (), params, u=u)
+        st = restated_sample(x, (), params, u=u, stable=True)
+        assert ref.kept == st.kept
+        # (the fp32 softmax sums the kept entries in vocab order, so the last bit may move)
+        np.testing.assert_allclose(np.sort(ref.probs.numpy()), np.sort(st.probs.numpy()), rtol=1e-6, atol=0)
+        fin = torch.isfinite(st.scores)
+        if st.pre_topp is not None and st.kept:
+            # the kept set is a prefix of (score descending, index ascending)
+            order = sorted(range(v), key=lambda i: (-float(st.pre_topp[i]), i))
+            assert set(order[:st.kept]) == set(torch.nonzero(fin).flatten().tolist())
+        # the top-N list: by value, equal values by index, then -inf entries by index
+        lp = st.scores.log_softmax(0)
+        want = sorted(range(v), key=lambda i: (-float(lp[i]), i))[:min(8, v)]
+        assert [i for i, _ in st.top_logprobs] == want
+
+
+def test_exact_top_p_cut_closed_forms():
+    """The exact (float64) cut: n equal scores keep floor(p*n) + 1 of them (exclusive mass
+    j/n <= p), the lowest indices; weights 2^-j (scores -j ln 2) keep the smallest J with
+    (1 - 2^-J) / (1 - 2^-n) > p."""
+    n = 1000
+    for p in (0.1, 0.25, 0.5, 0.731, 0.9, 0.99):
+        row = restated_sample(torch.zeros(n), (), P(temperature=1.0, top_p=p), u=0.5, stable=True)
+        k = math.floor(p * n) + 1
+        if abs(p * n - round(p * n)) > 1e-3:   # away from an exact multiple
+            assert row.topp_exact_kept == k
+            assert row.topp_exact_cut == (0.0, k - 1)
+    n = 40
+    x = torch.from_numpy((-np.arange(n) * math.log(2)).astype(np.float32))
+    xs = x.double().numpy()
+    w = np.exp(xs - xs[0])
+    for p in (0.3, 0.6, 0.8, 0.95, 0.999):
+        row = restated_sample(x, (), P(temperature=1.0, top_p=p), u=0.5, stable=True)
+        excl = (np.cumsum(w) - w) / w.sum()
+        assert row.topp_exact_kept == int((excl <= np.float32(p)).sum())
+        # closed form: excl(j) = (1 - 2^-j) / (1 - 2^-n) up to the fp32 rounding of -j ln 2
+        closed = next(j for j in range(1, n + 1) if (1 - 2.0 ** -j) / (1 - 2.0 ** -n) > np.float32(p))
+        assert row.topp_exact_kept == closed
+
+
+def _fake_gpu_output(rows, vocab, n):
+    """A BatchOutput holding exactly what the kernels' rules give, built from the stable
+    oracle: tokens, exact logprobs, kept counts with (cut score, cut index), top-N."""
+    from types import SimpleNamespace
+
+    from klsample import _lib
+    B = len(rows)
+    info = np.zeros(B, dtype=_lib.ROW_INFO_DTYPE)
+    top_ids = np.full((B, n), -1, np.int32)
+    top_lp = np.full((B, n), -np.inf, np.float32)
+    probs = np.zeros((B, vocab), np.float32)
+    for b, r in enumerate(rows):
+        s = r.scores.numpy()
+        fin = np.isfinite(s)
+        info['kept'][b] = int(fin.sum()) if not r.greedy else vocab
+        if not r.greedy:
+            cut = float(s[fin].min())
+            info['cut_score'][b] = cut
+            pre = (r.pre_topp if r.pre_topp is not None else r.scores).numpy()
+            ties = np.flatnonzero(pre == cut)
+            kept_ties = np.flatnonzero(s == cut)
+            info['cut_index'][b] = vocab if ties.size == kept_ties.size else int(kept_ties.max())
+            probs[b] = r.exact_probs.astype(np.float32)
+        for t, (i, v) in enumerate(r.top_logprobs):
+            top_ids[b, t], top_lp[b, t] = i, v
+    return SimpleNamespace(tokens=np.array([r.token_id for r in rows]),
+                           logprobs=np.array([r.exact_logprob for r in rows], np.float32),
+                           info=info, top_ids=top_ids, top_logprobs=top_lp,
+                           top=lambda b, c: tuple((int(top_ids[b, t]), float(top_lp[b, t]))
+                                                  for t in range(min(c, vocab, n)))), probs
+
+
+def test_parity_checker_accepts_the_kernel_rules_and_rejects_tie_swaps():
+    """compare() passes an output that follows the documented rules (built from the
+    oracle) on tie-heavy rows, and fails when a planted mistake in the oracle side swaps
+    a tied token, drops a kept entry, or perturbs one probability by 2e-5."""
+    from helpers import compare
+    rng = np.random.default_rng(32)
+    V, B = 3000, 12
+    x = torch.from_numpy((np.round(rng.standard_normal((B, V)) * 4) / 4).astype(np.float32))
+    params = [P(temperature=1.0, top_p=float(rng.uniform(0.5, 0.95)), logprobs=5) for _ in range(B - 2)]
+    params += [P(logprobs=5), P(temperature=0.7, top_k=30, logprobs=5)]
+    u = rng.random(B)
+    rows = sample_rows(x, None, params, u)
+    out, probs = _fake_gpu_output(rows, V, 5)
+    rep = compare(out, rows, params, probs=probs)
+    assert rep.ok(), rep.failures
+    assert rep.tie_rows > 0 and rep.exact == B
+    # plant: a tied neighbour of the token (same score, other index) for a row without margins
+    b = next(i for i, r in enumerate(rows) if not r.greedy and not r.boundary
+             and (r.scores == r.scores[r.token_id]).sum() > 1)
+    twin = int(torch.nonzero(rows[b].scores == rows[b].scores[rows[b].token_id]).flatten()[-1])
+    if twin == rows[b].token_id:
+        twin = int(torch.nonzero(rows[b].scores == rows[b].scores[rows[b].token_id]).flatten()[0])
+    bad = list(out.tokens)
+    bad[b] = twin
+    out.tokens = np.array(bad)
+    assert not compare(out, rows, params, probs=probs).ok()
+    out.tokens = np.array([r.token_id for r in rows])
+    # plant: one kept entry fewer
+    out.info['kept'][0] -= 1
+    assert not compare(out, rows, params, probs=probs).ok()
+    out.info['kept'][0] += 1
+    # plant: a probability off by 2e-5 relative
+    j = int(np.flatnonzero(probs[1] > 1e-3)[0])
+    probs[1, j] *= np.float32(1 + 2e-5)
+    assert not compare(out, rows, params, probs=probs).ok()

@@ -1,9 +1,17 @@
 """Parity of the HIP sampling path with the CPU oracle (MI355X only).
 
-Token ids must be bit-exact except on boundary rows (top-p cut, value tie across the
-cut, or CDF step within 1e-6), logprobs within 1e-5, kept sets equal, and the final
-probabilities within 1e-5 relative."""
+The oracle runs with the stable tie order (equal scores in ascending index order, the
+kernels' rule).  Token ids must be bit-exact on every row except boundary rows (top-p
+mass or CDF step within 1e-6 of the cut, where the token must still be kept); a value
+tie across the top-p cut is no exemption.  Kept sets are equal, logprobs and top-N
+values within 1e-5 of the exact (float64) log-softmax, top-N ids equal, and the final
+probabilities within 1e-5 relative of the exact softmax.
+
+With ``KLSAMPLE_PARITY_LOG`` set to a path, every comparison appends one JSON line of
+its counts (rows, boundary rows, mismatches, largest errors) to that file."""
+import json
 import math
+import os
 import sys
 
 import numpy as np
@@ -34,10 +42,15 @@ def run(logits, params, histories, uniforms, *, options=0, probs=False, n=None):
     return out
 
 
-def check(out, rows, params, probs=False):
+def check(out, rows, params, probs=False, label=None):
     rep = compare(out, rows, params, tol=TOL, probs=out.probs.cpu().numpy() if probs else None)
-    say(f'  rows={rep.rows} exact={rep.exact} boundary_rows={rep.boundary_rows} '
-        f'boundary_mismatches={rep.boundary_mismatches} failures={len(rep.failures)}')
+    counts = rep.counts()
+    say('  ' + ' '.join(f'{k}={v}' for k, v in counts.items()))
+    log = os.environ.get('KLSAMPLE_PARITY_LOG')
+    if log:
+        with open(log, 'a') as f:
+            f.write(json.dumps({'case': label or os.environ.get('PYTEST_CURRENT_TEST', '?').split(' ')[0],
+                                'probs': bool(probs), **counts}) + '\n')
     assert rep.ok(), '\n'.join(rep.failures[:20])
     return rep
 
@@ -52,20 +65,23 @@ def _with_logprobs(w, n):
 
 @pytest.mark.parametrize('name,batch,n,probs', [
     ('cpu_reference_b8', None, 0, True),
-    ('cpu_reference_b8', None, 5, False),
+    ('cpu_reference_b8', None, 5, True),
     ('latency_b1', None, 20, True),
     ('latency_b1_greedy', None, 3, True),
-    ('mixed_b64', None, 5, False),
-    ('throughput_b256_v128256', None, 0, False),
-    ('throughput_b256_v151936', None, 0, False),
-    ('tie_stress_b1024', None, 0, False),
+    ('mixed_b64', None, 5, True),
+    ('throughput_b256_v128256', None, 0, True),
+    ('throughput_b256_v151936', None, 3, True),
+    ('tie_stress_b1024', None, 4, True),
 ])
 def test_workload_parity(name, batch, n, probs):
+    """Every configured workload at full size, with probabilities: zero tie exemptions."""
     say(f'workload {name} batch={batch} logprobs={n}')
     w = _with_logprobs(workloads.make(name, batch=batch), n)
     rows = sample_rows(w.logits, w.histories, w.params, w.uniforms)
     out = run(w.logits, w.params, w.histories, w.uniforms, probs=probs)
-    check(out, rows, w.params, probs=probs)
+    rep = check(out, rows, w.params, probs=probs, label=f'workload {name} N={n}')
+    # ties across the top-p cut are compared like any other row
+    assert rep.exact + rep.boundary_mismatches == rep.rows
 
 
 @pytest.mark.parametrize('name,batch', [
@@ -101,15 +117,28 @@ CASES = golden_cases()
 
 @pytest.mark.parametrize('case', CASES, ids=[c['name'] for c in CASES])
 def test_reference_vectors_on_gpu(case):
+    """The GPU against the stable-order oracle (full parity), and against the vectors the
+    reference itself wrote.  Where the reference's unstable sort kept other members of a
+    tie at the top-p cut, its kept probabilities must still be the GPU's as a multiset."""
     say(f'golden {case["name"]}')
     p = case['params']
     params = SamplingParams(p.temperature, p.top_k, p.top_p, p.repetition_penalty, p.stop_token_ids, p.seed,
                             p.logprobs)
-    oracle_row = restated_sample(case['logits'], case['history'], params, u=case['u'])
+    stable_row = restated_sample(case['logits'], case['history'], params, u=case['u'], stable=True)
+    ref_row = restated_sample(case['logits'], case['history'], params, u=case['u'])
     out = run(case['logits'][None, :], [params], [case['history']], [case['u']], probs=True)
+    check(out, [stable_row], [params], probs=True, label=f'golden {case["name"]}')
     tok = int(out.tokens[0])
+    got = out.probs.cpu().numpy()[0]
+    if ref_row.topp_tie:
+        if case['probs'] is not None:
+            want = np.sort(case['probs'][case['probs'] > 0])
+            have = np.sort(got[got > 0])
+            assert want.size == have.size
+            np.testing.assert_allclose(have, want, rtol=TOL, atol=0)
+        return
     if tok != case['token']:
-        assert oracle_row.boundary and not oracle_row.greedy, (tok, case['token'])
+        assert ref_row.boundary and not ref_row.greedy, (tok, case['token'])
         return
     assert close(float(out.logprobs[0]), case['logprob'], TOL)
     assert (tok in params.stop_token_ids) == case['stopped']
@@ -117,8 +146,7 @@ def test_reference_vectors_on_gpu(case):
     assert len(got_top) == len(case['top'])
     for (gi, gv), (wi, wv) in zip(got_top, case['top']):
         assert close(gv, wv, TOL)
-    if case['probs'] is not None and not oracle_row.boundary:
-        got = out.probs.cpu().numpy()[0]
+    if case['probs'] is not None and not ref_row.boundary:
         np.testing.assert_array_equal(got > 0, case['probs'] > 0)
         m = case['probs'] > 1e-30
         np.testing.assert_allclose(got[m], case['probs'][m], rtol=TOL, atol=0)
