@@ -20,8 +20,9 @@ so that on the same fp32 inputs it produces the same scores bit for bit, and add
   (``serving/sampling.py:57``) and takes its top-N with ``topk`` (``:62``), so which of
   several equal scores is kept at the top-p cut, and the order of equal top-N entries,
   are implementation-defined there.  With ``stable=True`` equal scores are taken in
-  ascending index order in both places, and top-N slots past the kept set list the
-  smallest ids whose final score is ``-inf``.  The kept *count*, every probability and
+  ascending index order in both places, the top-N list is ordered by final score (two
+  scores one ulp apart can share an fp32 logprob), and top-N slots past the kept set
+  list the smallest ids whose final score is ``-inf``.  The kept *count*, every probability and
   every logprob are the reference's; only the identities among equal scores are fixed.  The reference's fp32 ``softmax`` over a 151,936-entry row sums
   to ``1 + delta`` with ``|delta|`` up to ~3e-5 (measured: the last element of its own
   ``cumsum``), so its cut can differ from the exact one by a few tokens; the top-p
@@ -204,10 +205,11 @@ def restated_sample(logits: torch.Tensor, history=(), params=None, *, u: float |
     if not count:
         top = ()
     elif stable:
-        # equal values in index order; past the kept set the -inf entries in index order
-        # are the smallest ids not listed before them
-        v, i = log_probabilities.sort(descending=True, stable=True)
-        top = tuple((int(a), float(b)) for b, a in zip(v[:count], i[:count]))
+        # ordered by final score, equal scores in index order (two distinct scores may
+        # round to one fp32 logprob; the score still orders them); past the kept set the
+        # -inf entries in index order are the smallest ids not listed before them
+        order = scores.sort(descending=True, stable=True).indices[:count]
+        top = tuple((int(a), float(log_probabilities[a])) for a in order)
     else:
         top = tuple((int(i), float(v)) for v, i in zip(*log_probabilities.topk(count)))   # :62
     row.token_id = token

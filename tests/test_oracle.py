@@ -286,10 +286,12 @@ def test_stable_tie_order_keeps_the_reference_count_and_lowest_indices():
             # the kept set is a prefix of (score descending, index ascending)
             order = sorted(range(v), key=lambda i: (-float(st.pre_topp[i]), i))
             assert set(order[:st.kept]) == set(torch.nonzero(fin).flatten().tolist())
-        # the top-N list: by value, equal values by index, then -inf entries by index
-        lp = st.scores.log_softmax(0)
-        want = sorted(range(v), key=lambda i: (-float(lp[i]), i))[:min(8, v)]
+        # the top-N list: by final score, equal scores by index, then -inf entries by index
+        sc = st.scores
+        want = sorted(range(v), key=lambda i: (-float(sc[i]), i))[:min(8, v)]
         assert [i for i, _ in st.top_logprobs] == want
+        lp = sc.log_softmax(0)
+        assert [b for _, b in st.top_logprobs] == [float(lp[i]) for i in want]
 
 
 def test_exact_top_p_cut_closed_forms():
@@ -383,3 +385,16 @@ def test_parity_checker_accepts_the_kernel_rules_and_rejects_tie_swaps():
     j = int(np.flatnonzero(probs[1] > 1e-3)[0])
     probs[1, j] *= np.float32(1 + 2e-5)
     assert not compare(out, rows, params, probs=probs).ok()
+
+
+def test_stable_top_n_orders_by_score_when_logprobs_round_together():
+    """Two scores one ulp apart share an fp32 logprob over a wide row; the higher score
+    is still listed first (the kernels' order), whatever its index."""
+    x = torch.zeros(100_000)
+    c = np.float32(0.01)
+    x[7] = float(c)
+    x[3] = float(np.nextafter(c, np.float32(-1)))
+    row = restated_sample(x, (), P(logprobs=3), stable=True)
+    lp = x.log_softmax(0)
+    assert float(lp[7]) == float(lp[3])
+    assert [i for i, _ in row.top_logprobs] == [7, 3, 0]
