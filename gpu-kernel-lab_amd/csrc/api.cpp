@@ -128,7 +128,13 @@ int klsample_workspace_init(void *workspace, size_t workspace_bytes, void *strea
     return ok();
 }
 
-int klsample_run(const klsample_batch *b, void *stream) {
+}  // extern "C"
+
+namespace {
+
+// Validates everything of a call but its workspace and fills the kernel arguments (the
+// workspace pointers excepted).  Host only: no HIP call.
+int prepare(const klsample_batch *b, kls::Plan *plan, kls::Args *args) {
     if (b == nullptr) return fail(KLSAMPLE_ERR_INVALID_ARGUMENT, "batch must not be NULL");
     int st = check_sizes(b->batch, b->vocab, b->dtype, b->max_top_k, b->num_logprobs);
     if (st != KLSAMPLE_OK) return st;
@@ -145,17 +151,11 @@ int klsample_run(const klsample_batch *b, void *stream) {
         return fail(KLSAMPLE_ERR_INVALID_ARGUMENT, "history_ids must not be NULL when history_offsets is given");
     if ((b->options & ~(uint32_t)KLSAMPLE_OPT_FORCE_DENSE) != 0)
         return fail(KLSAMPLE_ERR_INVALID_ARGUMENT, "unknown option bits 0x%x", b->options);
-    if (b->workspace == nullptr) return fail(KLSAMPLE_ERR_WORKSPACE, "workspace must not be NULL");
-    if (((uintptr_t)b->workspace & 255u) != 0) return fail(KLSAMPLE_ERR_WORKSPACE, "workspace must be 256-byte aligned");
-    kls::Plan plan;
-    if (!kls::make_plan(b->batch, b->vocab, b->dtype, b->max_top_k, b->num_logprobs, &plan))
+    if (!kls::make_plan(b->batch, b->vocab, b->dtype, b->max_top_k, b->num_logprobs, plan))
         return fail(KLSAMPLE_ERR_INVALID_ARGUMENT, "batch * chunks exceeds the grid limit");
-    if (b->workspace_bytes < plan.total)
-        return fail(KLSAMPLE_ERR_WORKSPACE, "workspace too small: %zu bytes given, %zu needed", b->workspace_bytes,
-                    plan.total);
 
     const size_t esize = b->dtype == KLSAMPLE_FLOAT32 ? 4 : 2;
-    kls::Args a;
+    kls::Args &a = *args;
     a.logits = b->logits;
     a.row_stride = b->row_stride;
     a.B = b->batch;
@@ -171,23 +171,61 @@ int klsample_run(const klsample_batch *b, void *stream) {
     a.top_lp = b->top_logprobs;
     a.probs = b->probs;
     a.row_info = b->row_info;
-    unsigned char *ws = static_cast<unsigned char *>(b->workspace);
+    a.ypitch = plan->ypitch;
+    a.E = plan->elems;
+    a.C = plan->chunk;
+    a.S = plan->chunks;
+    a.cand_cap = plan->cand_cap;
+    a.vec_ok = (((uintptr_t)b->logits & 15u) == 0 && ((size_t)b->row_stride * esize) % 16 == 0) ? 1 : 0;
+    a.xcd_map = (b->batch % 8 == 0) ? 1 : 0;
+    return KLSAMPLE_OK;
+}
+
+// Points the kernel arguments at a workspace laid out by `plan` and launches.
+int launch(const klsample_batch *b, const kls::Plan &plan, kls::Args &a, void *workspace, void *stream) {
+    unsigned char *ws = static_cast<unsigned char *>(workspace);
     a.stats = reinterpret_cast<kls::ChunkStat *>(ws + plan.off_stats);
     a.cands = reinterpret_cast<kls::Cand *>(ws + plan.off_cands);
     a.rows = reinterpret_cast<klsample_row_info *>(ws + plan.off_rows);
     a.ybuf = reinterpret_cast<float *>(ws + plan.off_ybuf);
-    a.ypitch = plan.ypitch;
-    a.E = plan.elems;
-    a.C = plan.chunk;
-    a.S = plan.chunks;
-    a.cand_cap = plan.cand_cap;
-    a.vec_ok = (((uintptr_t)b->logits & 15u) == 0 && ((size_t)b->row_stride * esize) % 16 == 0) ? 1 : 0;
-    a.xcd_map = (b->batch % 8 == 0) ? 1 : 0;
-
     const hipError_t e = kls::launch_sample(a, b->dtype, static_cast<hipStream_t>(stream),
                                            g_phases_on ? &g_phases : nullptr);
     if (e != hipSuccess) return fail(KLSAMPLE_ERR_HIP, "kernel launch failed: %s", hipGetErrorString(e));
     return ok();
+}
+
+}  // namespace
+
+extern "C" {
+
+int klsample_run(const klsample_batch *b, void *stream) {
+    kls::Plan plan;
+    kls::Args a;
+    const int st = prepare(b, &plan, &a);
+    if (st != KLSAMPLE_OK) return st;
+    if (b->workspace == nullptr) return fail(KLSAMPLE_ERR_WORKSPACE, "workspace must not be NULL");
+    if (((uintptr_t)b->workspace & 255u) != 0) return fail(KLSAMPLE_ERR_WORKSPACE, "workspace must be 256-byte aligned");
+    if (b->workspace_bytes < plan.total)
+        return fail(KLSAMPLE_ERR_WORKSPACE, "workspace too small: %zu bytes given, %zu needed", b->workspace_bytes,
+                    plan.total);
+    return launch(b, plan, a, b->workspace, stream);
+}
+
+int klsample_run_noalloc(const klsample_batch *b, void *stream) {
+    kls::Plan plan;
+    kls::Args a;
+    const int st = prepare(b, &plan, &a);
+    if (st != KLSAMPLE_OK) return st;
+    if (b->workspace != nullptr || b->workspace_bytes != 0)
+        return fail(KLSAMPLE_ERR_WORKSPACE, "klsample_run_noalloc takes no workspace (workspace must be NULL and "
+                    "workspace_bytes 0)");
+    if (plan.total > kls::kScratchBytes)
+        return fail(KLSAMPLE_ERR_WORKSPACE, "this call needs %zu bytes of workspace; the static scratch holds %zu "
+                    "(use klsample_run with a caller workspace)", plan.total, kls::kScratchBytes);
+    void *ws = nullptr;
+    const hipError_t e = kls::scratch_workspace(static_cast<hipStream_t>(stream), &ws);
+    if (e != hipSuccess) return fail(KLSAMPLE_ERR_HIP, "scratch address lookup failed: %s", hipGetErrorString(e));
+    return launch(b, plan, a, ws, stream);
 }
 
 }  // extern "C"

@@ -84,4 +84,10 @@ struct PhaseEvents {
 hipError_t launch_sample(const Args &args, int32_t dtype, hipStream_t stream, const PhaseEvents *phases);
 hipError_t launch_zero_fill(void *ptr, size_t bytes, hipStream_t stream);
 
+// Workspace of klsample_run_noalloc: a static device array of kScratchBytes per GPU.
+// scratch_workspace returns its device address on the device of `stream` (the current
+// device for the NULL stream), taken once per device with hipGetSymbolAddress.
+constexpr size_t kScratchBytes = KLSAMPLE_NOALLOC_SCRATCH_BYTES;
+hipError_t scratch_workspace(hipStream_t stream, void **ptr);
+
 }  // namespace kls

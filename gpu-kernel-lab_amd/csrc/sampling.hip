@@ -33,6 +33,7 @@
 #include <math.h>
 #include <stdint.h>
 
+#include <mutex>
 #include <type_traits>
 
 #include "internal.h"
@@ -3062,6 +3063,43 @@ hipError_t launch_sample(const Args &a, int32_t dtype, hipStream_t s, const Phas
         }
     }
     return hipErrorInvalidValue;
+}
+
+// ---------------------------------------------------------------------------------
+// The workspace of klsample_run_noalloc: one array per GPU, held until the process
+// ends.  In host code `scratch` names a host-side stand-in, not device memory: its
+// device address comes from hipGetSymbolAddress, taken once per device (with that
+// device current) and kept, and only that address is handed to kernels.  No call
+// needs the array cleared: every workspace byte a call reads was written earlier in
+// the same call.  Calls that overlap on one GPU share it and race.
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+constexpr int kScratchDevices = 64;
+
+hipError_t scratch_workspace(hipStream_t s, void **ptr) {
+    static std::mutex mu;
+    static void *addr[kScratchDevices] = {};
+    int dev = -1;
+    hipError_t e = (s != nullptr) ? hipStreamGetDevice(s, &dev) : hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev < 0 || dev >= kScratchDevices) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lock(mu);
+    if (addr[dev] == nullptr) {
+        int cur = -1;
+        if ((e = hipGetDevice(&cur)) != hipSuccess) return e;
+        if (cur != dev && (e = hipSetDevice(dev)) != hipSuccess) return e;
+        void *p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (cur != dev) {
+            const hipError_t back = hipSetDevice(cur);
+            if (e == hipSuccess) e = back;
+        }
+        if (e != hipSuccess) return e;
+        if (p == nullptr) return hipErrorInvalidSymbol;
+        addr[dev] = p;
+    }
+    *ptr = addr[dev];
+    return hipSuccess;
 }
 
 hipError_t launch_zero_fill(void *ptr, size_t bytes, hipStream_t s) {

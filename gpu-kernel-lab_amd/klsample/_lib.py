@@ -35,7 +35,8 @@ MAX_BATCH = 65536
 MAX_VOCAB = 1 << 24
 
 EXPORTS = ('klsample_abi_version', 'klsample_workspace_size', 'klsample_workspace_init',
-           'klsample_run', 'klsample_set_phase_events', 'klsample_last_error')
+           'klsample_run', 'klsample_run_noalloc', 'klsample_set_phase_events', 'klsample_last_error')
+NOALLOC_SCRATCH_BYTES = 64 << 20
 
 # klsample_row_params, 32 bytes
 ROW_PARAMS_DTYPE = np.dtype([
@@ -108,6 +109,8 @@ def load(path: Path | str | None = None) -> ctypes.CDLL:
         lib.klsample_workspace_init.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
         lib.klsample_run.restype = ctypes.c_int
         lib.klsample_run.argtypes = [ctypes.POINTER(Batch), ctypes.c_void_p]
+        lib.klsample_run_noalloc.restype = ctypes.c_int
+        lib.klsample_run_noalloc.argtypes = [ctypes.POINTER(Batch), ctypes.c_void_p]
         lib.klsample_set_phase_events.restype = ctypes.c_int
         lib.klsample_set_phase_events.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_int32]
         version = lib.klsample_abi_version()

@@ -123,6 +123,21 @@ int klsample_workspace_init(void *workspace, size_t workspace_bytes, void *strea
  * exceeds uniform * total. */
 int klsample_run(const klsample_batch *batch, void *stream);
 
+/* Bytes of the static device scratch klsample_run_noalloc works in (per GPU). */
+#define KLSAMPLE_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
+
+/* klsample_run without a caller workspace and without any allocation: no reference
+ * counterpart; for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  Same arguments,
+ * results and status codes as klsample_run, except that batch->workspace must be NULL
+ * and batch->workspace_bytes 0: the call works in a static device array of
+ * KLSAMPLE_NOALLOC_SCRATCH_BYTES per GPU, held from the library's first use on that
+ * GPU until the process ends.  A call whose klsample_workspace_size exceeds that
+ * returns KLSAMPLE_ERR_WORKSPACE before touching the device.  Every call on one GPU
+ * shares that GPU's array, so calls that overlap on one GPU (other streams or host
+ * threads) race: issue them on one stream.  Calls no hipMalloc/hipFree. */
+int klsample_run_noalloc(const klsample_batch *batch, void *stream);
+
 /* Diagnostic timing; no reference counterpart.  With count in [1, 4], every later
  * klsample_run issued from this thread records events[i] (hipEvent_t handles owned by
  * the caller, NULL entries skipped) on its stream: events[0] before the streaming pass

@@ -165,3 +165,29 @@ def test_errors_map_to_python_exceptions(lib):
 def test_row_params_dtype_is_32_bytes():
     assert _lib.ROW_PARAMS_DTYPE.itemsize == 32 and _lib.ROW_INFO_DTYPE.itemsize == 32
     assert np.zeros(1, _lib.ROW_PARAMS_DTYPE).nbytes == 32
+
+
+@pytest.mark.parametrize('mutate,status,needle', [
+    (lambda b: setattr(b, 'batch', 0), _lib.ERR_INVALID_ARGUMENT, 'batch'),
+    (lambda b: setattr(b, 'logits', None), _lib.ERR_INVALID_ARGUMENT, 'logits'),
+    (lambda b: setattr(b, 'num_logprobs', 3), _lib.ERR_INVALID_ARGUMENT, 'top_ids'),
+    (lambda b: setattr(b, 'workspace', 0x100000), _lib.ERR_WORKSPACE, 'takes no workspace'),
+    (lambda b: setattr(b, 'workspace_bytes', 4096), _lib.ERR_WORKSPACE, 'takes no workspace'),
+    (lambda b: (setattr(b, 'batch', 4096), setattr(b, 'vocab', 151936), setattr(b, 'row_stride', 151936)),
+     _lib.ERR_WORKSPACE, 'static scratch holds'),
+])
+def test_noalloc_rejects_before_touching_the_device(lib, mutate, status, needle):
+    """The no-allocation entry point validates like klsample_run, takes no workspace, and
+    refuses a call needing more than its static scratch, all before any HIP call."""
+    b = _valid_batch()
+    b.workspace = None
+    b.workspace_bytes = 0
+    mutate(b)
+    assert lib.klsample_run_noalloc(ctypes.byref(b), None) == status
+    assert needle in _lib.last_error(lib)
+    assert lib.klsample_run_noalloc(None, None) == _lib.ERR_INVALID_ARGUMENT
+
+
+def test_noalloc_capacity_matches_header():
+    m = re.search(r'#define KLSAMPLE_NOALLOC_SCRATCH_BYTES \(\(size_t\)(\d+) << (\d+)\)', HEADER.read_text())
+    assert m and int(m.group(1)) << int(m.group(2)) == _lib.NOALLOC_SCRATCH_BYTES
