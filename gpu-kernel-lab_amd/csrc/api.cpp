@@ -88,6 +88,8 @@ bool make_plan(int32_t batch, int32_t vocab, int32_t dtype, int32_t max_top_k, i
     // pass reads (they read up to vocab rounded up to 4)
     p->ypitch = (int32_t)align_up((size_t)vocab + 1, 4);
     p->off_ybuf = off;    off = align_up(off + B * (size_t)p->ypitch * sizeof(float), 256);
+    // histograms of top-p chunks (written only by those)
+    p->off_hist = off;    off = align_up(off + B * S * (size_t)kWideBins * sizeof(unsigned long long), 256);
     p->total = off;
     return (int64_t)batch * p->chunks <= INT32_MAX;
 }
@@ -178,6 +180,7 @@ int prepare(const klsample_batch *b, kls::Plan *plan, kls::Args *args) {
     a.cand_cap = plan->cand_cap;
     a.vec_ok = (((uintptr_t)b->logits & 15u) == 0 && ((size_t)b->row_stride * esize) % 16 == 0) ? 1 : 0;
     a.xcd_map = (b->batch % 8 == 0) ? 1 : 0;
+    a.wide_split = ((int64_t)b->batch * plan->chunks <= kls::kWideSplitGroups) ? 1 : 0;
     return KLSAMPLE_OK;
 }
 
@@ -188,6 +191,7 @@ int launch(const klsample_batch *b, const kls::Plan &plan, kls::Args &a, void *w
     a.cands = reinterpret_cast<kls::Cand *>(ws + plan.off_cands);
     a.rows = reinterpret_cast<klsample_row_info *>(ws + plan.off_rows);
     a.ybuf = reinterpret_cast<float *>(ws + plan.off_ybuf);
+    a.hist = reinterpret_cast<unsigned long long *>(ws + plan.off_hist);
     const hipError_t e = kls::launch_sample(a, b->dtype, static_cast<hipStream_t>(stream),
                                            g_phases_on ? &g_phases : nullptr);
     if (e != hipSuccess) return fail(KLSAMPLE_ERR_HIP, "kernel launch failed: %s", hipGetErrorString(e));

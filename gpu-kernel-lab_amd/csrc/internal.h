@@ -17,6 +17,25 @@ constexpr int kMaxLogprobs = 256;      // largest supported num_logprobs
 constexpr int kMaxBatch = 65536;       // rows per call
 constexpr int kMaxChunksLds = 4096;    // chunks per row the candidate combine indexes in LDS
 
+// Chunks of top-p rows also write a log-space histogram and their final scores, for
+// rows whose kept set reaches past the candidates: bin j of a chunk holds the
+// entries with floor(y * kWideCells) == G - j, G = floor(m_c * kWideCells) for the
+// chunk max m_c (the last bin everything further down).  Each bin is one 64-bit word:
+// the entry count above bit kWideCountShift, below it the sum of the entries'
+// fixed-point weights exp(y - G / kWideCells) in units of 2^-kWideMassBits.
+constexpr int kWideBins = 1024;
+constexpr float kWideCells = 32.f;       // bins per unit of score (natural log)
+constexpr int kWideCountShift = 50;
+constexpr int kWideMassBits = 36;
+constexpr float kWideMaxScore = 262144.f; // |chunk max| below this keeps the grid exact in fp32
+constexpr int kWideMaxChunks = 512;      // chunks per row the wide resolution indexes in LDS
+constexpr int kWideSplitGroups = 512;    // at most this many (row, chunk) workgroups: the
+                                         // histograms come from a second workgroup per chunk
+
+// ChunkStat::flags
+constexpr int32_t kChunkOverflow = 1;    // candidates exceeded the slot capacity
+constexpr int32_t kChunkWide = 2;        // histogram and final scores written (top-p chunk)
+
 // Row classes; every row of a batch is one of these.
 enum RowMode : int { kGreedy = 0, kTopK = 1, kTopP = 2, kFull = 3 };
 
@@ -27,7 +46,7 @@ struct ChunkStat {
     float y_thr;      // every element of the chunk with score >= y_thr is a candidate
     int32_t ncand;    // candidates written (capped at the slot capacity)
     double z;         // sum of exp(s - m) over the chunk
-    int32_t overflow; // candidates exceeded the slot capacity
+    int32_t flags;    // kChunkOverflow | kChunkWide
     int32_t nfinite;  // elements with a finite score (greedy / top-p / full rows)
 };
 
@@ -43,7 +62,7 @@ struct Plan {
     int32_t chunks;   // chunks per row (S)
     int32_t cand_cap; // candidate slots per chunk
     int32_t ypitch;   // floats per row of the dense path's score buffer
-    size_t off_stats, off_cands, off_rows, off_ybuf, total;
+    size_t off_stats, off_cands, off_rows, off_ybuf, off_hist, total;
 };
 
 bool make_plan(int32_t batch, int32_t vocab, int32_t dtype, int32_t max_top_k, int32_t num_logprobs,
@@ -67,11 +86,13 @@ struct Args {
     ChunkStat *stats;
     Cand *cands;           // per (row, chunk): cand_cap slots
     klsample_row_info *rows;
-    float *ybuf;           // dense row path: per row ypitch final scores
+    float *ybuf;           // per row ypitch final scores (top-p chunks, dense row path)
+    unsigned long long *hist;  // per (row, chunk) kWideBins histogram words of a top-p chunk
     int32_t ypitch;        // vocab + 1 rounded up to a multiple of 4 (the last float is a spare slot)
     int32_t E, C, S, cand_cap;
     int32_t vec_ok;   // 16-byte vector loads are legal for every row
     int32_t xcd_map;  // place all chunks of a row on one XCD
+    int32_t wide_split;  // top-p chunks' histograms from a second workgroup each (small grids)
 };
 
 // Caller-owned hipEvent_t handles recorded around the kernels of a call (diagnostics):

@@ -68,8 +68,9 @@ __device__ __forceinline__ float exp_fast(float d) {
 // are exact and independent of their order.  w * 2^40 (w = exp(y - m) <= 1) is exact in
 // fp32, rounded half-to-even to an integer there, and split into two 32-bit halves, each
 // converted exactly: the value of round((double)w * 2^40), in full-rate fp32 operations.
+template <int kBits = 40>
 __device__ __forceinline__ unsigned long long weight_fix(float y, float m) {
-    const float f = __builtin_rintf(exp_fast(y - m) * 1099511627776.0f);
+    const float f = __builtin_rintf(exp_fast(y - m) * (float)(1ull << kBits));
     const float h = __builtin_truncf(f * 2.3283064365386963e-10f);   // f / 2^32
     const float lo = __builtin_fmaf(h, -4294967296.0f, f);            // f - h * 2^32, exact
     return ((unsigned long long)(uint32_t)h << 32) | (uint32_t)lo;
@@ -509,39 +510,28 @@ __device__ __forceinline__ float chunk_bound(const float (&x)[E], int K, int cn,
 // for the entries it contains; each thread visits a disjoint subset.
 
 // The row's candidates in their per-chunk slots: chunk c holds cnt[c] entries (cnt in
-// LDS).  Waves take chunks round robin, four at a time, and lanes take a chunk's
-// entries, so the loads of four chunks are in flight together.
+// LDS).  Waves take chunks round robin and lanes a chunk's entries, eight loads in
+// flight per lane (addresses clamped into the chunk's entries rather than predicated),
+// so a chunk of up to 512 candidates is one round trip.
 struct CandSource {
     const Cand *cands;
     const int *cnt;
     int S, cap;
     float lo;
     template <class F>
-    __device__ __forceinline__ void visit(uint2 e, F &f) const {
-        const float y = __uint_as_float(e.x);
-        if (y >= lo) f(fkey(y), (int)e.y, y);
-    }
-    template <class F>
     __device__ __forceinline__ void each(F f) const {
         const int lane = lane_id();
-        for (int c = wave_id(); c < S; c += 4 * kWaves) {
-            uint2 e[4];
-            bool v[4];
+        for (int c = wave_id(); c < S; c += kWaves) {
+            const int n = cnt[c];
+            const uint2 *p = reinterpret_cast<const uint2 *>(cands + (size_t)c * cap);
+            for (int j0 = 0; j0 < n; j0 += 64 * 8) {
+                uint2 e[8];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int cc = c + i * kWaves;
-                v[i] = cc < S && lane < cnt[cc];
-                if (v[i]) e[i] = reinterpret_cast<const uint2 *>(cands + (size_t)cc * cap)[lane];
-            }
+                for (int u = 0; u < 8; ++u) e[u] = p[min(j0 + u * 64 + lane, n - 1)];
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
-                if (v[i]) visit(e[i], f);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int cc = c + i * kWaves;
-                if (cc < S) {
-                    const uint2 *p = reinterpret_cast<const uint2 *>(cands + (size_t)cc * cap);
-                    for (int j = lane + 64; j < cnt[cc]; j += 64) visit(p[j], f);
+                for (int u = 0; u < 8; ++u) {
+                    const float y = __uint_as_float(e[u].x);
+                    if (j0 + u * 64 + lane < n && y >= lo) f(fkey(y), (int)e[u].y, y);
                 }
             }
         }
@@ -1045,7 +1035,7 @@ __device__ __forceinline__ ChunkStat load_stat(const ChunkStat *p) {
     s.y_thr = __uint_as_float(u.z);
     s.ncand = (int32_t)u.w;
     s.z = __hiloint2double((int)v.y, (int)v.x);
-    s.overflow = (int32_t)v.z;
+    s.flags = (int32_t)v.z;
     s.nfinite = (int32_t)v.w;
     return s;
 }
@@ -1295,6 +1285,65 @@ __device__ __forceinline__ int dense_topn(const DenseSource &src, int N, unsigne
     return want;
 }
 
+// Top-p cut inside a sorted run of entries: G[0..n) (n >= 1) sorted best first, every
+// entry scoring above them already counted (`above` fixed-point mass, `above_count`
+// entries).  Walking from the top, the first entry whose inclusive mass exceeds
+// `target` crosses; of its group of equal scores, entries are kept in index order while
+// their exclusive mass does not exceed `target` (at least one).  If no entry crosses
+// (rounding), the last entry is taken as the crossing one.  All threads receive the
+// result.
+__device__ __forceinline__ void cut_in_sorted(const unsigned long long *G, int n, unsigned long long above,
+                                              uint32_t above_count, double target, float m, TopPCut &out, Misc &ms) {
+    if (wave_id() == 0) {
+        const int l = lane_id();
+        unsigned long long run = above;
+        int j = -1;
+        unsigned long long incl_j = 0ull;
+        for (int i0 = 0; i0 < n && j < 0; i0 += 64) {
+            const int i = i0 + l;
+            const unsigned long long w = i < n ? weight_fix(desc_key_y(G[i]), m) : 0ull;
+            const unsigned long long incl = run + wave_incl_scan(w);
+            const unsigned long long bal = __ballot(i < n && (double)incl > target);
+            if (bal != 0ull) {
+                const int fl = __ffsll((long long)bal) - 1;
+                j = i0 + fl;
+                incl_j = readlane(incl, fl);
+            }
+            run = readlane(incl, 63);
+        }
+        if (j < 0) j = n - 1, incl_j = run;   // rounding: take the last entry
+        // the group of equal scores around j: [gs, ge)
+        const float yg = desc_key_y(G[j]);
+        const unsigned long long kg = (unsigned long long)(~fkey(yg)) << 32;
+        int lo = 0, hi = j;
+        while (lo < hi) { const int mid = (lo + hi) >> 1; if (G[mid] < kg) lo = mid + 1; else hi = mid; }
+        const int gs = lo;
+        lo = j + 1; hi = n;
+        while (lo < hi) { const int mid = (lo + hi) >> 1; if ((G[mid] >> 32) == (kg >> 32)) lo = mid + 1; else hi = mid; }
+        const int ge = lo;
+        const unsigned long long wt = weight_fix(yg, m);
+        const unsigned long long above_g = incl_j - (unsigned long long)(j - gs + 1) * wt;
+        const int count = ge - gs;
+        int keep = count;
+        if (wt > 0ull) {
+            const double room = target - (double)above_g;
+            const double k = floor(room / (double)wt) + 1.0;
+            keep = (int)fmin((double)count, fmax(1.0, k));
+        }
+        if (l == 0) {
+            TopPCut r;
+            r.cut = yg;
+            r.cut_idx = (keep < count) ? desc_key_idx(G[gs + keep - 1]) : 0x7fffffff;
+            r.kept = (int)above_count + gs + keep;
+            r.zf = above_g + (unsigned long long)keep * wt;
+            ms.topp = r;
+        }
+    }
+    __syncthreads();
+    out = ms.topp;
+    __syncthreads();
+}
+
 // Top-p cut over a dense source by a mass histogram in log space: bin b holds the
 // kept entries with (m - y) * 64 in [b, b + 1) (the last bin everything further
 // down), which orders bins like scores.  The bin where the running mass from the top
@@ -1377,54 +1426,7 @@ __device__ __forceinline__ int topp_cut_bins(const DenseSource &src, float m, fl
     __syncthreads();
     const int n = min(ms.ncand, cap);
     sort_keys(G, n, ms.part);
-    if (wave_id() == 0) {
-        const double target = (double)top_p * (double)zk;
-        const int l = lane_id();
-        unsigned long long run = above;
-        int j = -1;
-        unsigned long long incl_j = 0ull;
-        for (int i0 = 0; i0 < n && j < 0; i0 += 64) {
-            const int i = i0 + l;
-            const unsigned long long w = i < n ? weight_fix(desc_key_y(G[i]), m) : 0ull;
-            const unsigned long long incl = run + wave_incl_scan(w);
-            const unsigned long long bal = __ballot(i < n && (double)incl > target);
-            if (bal != 0ull) {
-                const int fl = __ffsll((long long)bal) - 1;
-                j = i0 + fl;
-                incl_j = readlane(incl, fl);
-            }
-            run = readlane(incl, 63);
-        }
-        if (j < 0) j = n - 1, incl_j = run;   // rounding: take the bin's last entry
-        // the group of equal scores around j: [gs, ge)
-        const float yg = desc_key_y(G[j]);
-        const unsigned long long kg = (unsigned long long)(~fkey(yg)) << 32;
-        int lo = 0, hi = j;
-        while (lo < hi) { const int mid = (lo + hi) >> 1; if (G[mid] < kg) lo = mid + 1; else hi = mid; }
-        const int gs = lo;
-        lo = j + 1; hi = n;
-        while (lo < hi) { const int mid = (lo + hi) >> 1; if ((G[mid] >> 32) == (kg >> 32)) lo = mid + 1; else hi = mid; }
-        const int ge = lo;
-        const unsigned long long wt = weight_fix(yg, m);
-        const unsigned long long above_g = incl_j - (unsigned long long)(j - gs + 1) * wt;
-        const int count = ge - gs;
-        int keep = count;
-        if (wt > 0ull) {
-            const double room = target - (double)above_g;
-            const double k = floor(room / (double)wt) + 1.0;
-            keep = (int)fmin((double)count, fmax(1.0, k));
-        }
-        if (l == 0) {
-            out.cut = yg;
-            out.cut_idx = (keep < count) ? desc_key_idx(G[gs + keep - 1]) : 0x7fffffff;
-            out.kept = (int)above_count + gs + keep;
-            out.zf = above_g + (unsigned long long)keep * wt;
-            ms.topp = out;
-        }
-    }
-    __syncthreads();
-    out = ms.topp;
-    __syncthreads();
+    cut_in_sorted(G, n, above, above_count, (double)top_p * (double)zk, m, out, ms);
     return 1;
 }
 
@@ -1605,6 +1607,531 @@ __device__ __forceinline__ void dense_resolve(const Args &a, int row, const klsa
     write_row(a, row, mode, r, count, ms);
 }
 
+// A top-p row whose kept set reaches past the candidates; every chunk wrote its
+// histogram and its final scores (wide_chunk).
+//  1. The chunk histograms are merged into one over the row: chunk c's bin jc is row
+//     bin jc + (G - G_c) (G of the row max m), its mass converted to units of 2^-40
+//     relative to m (one rounding per chunk bin, identical wherever it is repeated).
+//  2. The cut bin is the first whose running mass from the top exceeds p * total.
+//  3. Per chunk: the mass of its bins above the cut bin.
+//  4. One pass over the row's scores gathers the cut bin's entries, split 256 ways by
+//     score; the crossing part, sorted, gives the crossing entry and the ties it keeps
+//     (cut_in_sorted).
+//  5. Each chunk's kept mass (step 3 and its kept cut-bin entries) gives the chunk where
+//     the kept mass in vocab order crosses u * total; that chunk's scores are walked.
+// `want` top-N entries are in ms.topn_*.  `ctab` holds kWideMaxChunks * 20 bytes and
+// `raw` (kWideCross + kWideList) * 8 bytes of LDS.  Returns false, writing nothing, when
+// the row cannot be resolved this way (cut in the last bin, a crossing part too large
+// for LDS); dense_resolve runs.
+constexpr int kWideList = 4096;    // cut-bin entries held in LDS
+constexpr int kWideCross = 2048;   // entries of the crossing part of the cut bin
+
+__device__ __forceinline__ bool wide_resolve(const Args &a, int row, const klsample_row_params &p, int mode, float m,
+                                             int want, unsigned char *raw, unsigned long long *ctab, Misc &ms) {
+    const int S = a.S, V = a.V, C = a.C, tid = threadIdx.x;
+    const ChunkStat *st = a.stats + (size_t)row * S;
+    const unsigned long long *hist = a.hist + (size_t)row * S * kWideBins;
+    const float *yb = a.ybuf + (size_t)row * a.ypitch;
+    uint32_t *hc = reinterpret_cast<uint32_t *>(raw);                                      // row bin counts
+    unsigned long long *hm = reinterpret_cast<unsigned long long *>(raw + kWideBins * 4);  // row bin masses
+    unsigned long long *D = reinterpret_cast<unsigned long long *>(raw);                   // crossing part (after 2)
+    unsigned long long *L = reinterpret_cast<unsigned long long *>(raw + kWideCross * 8);  // cut-bin entries
+    static_assert(kWideBins * 12 <= kWideCross * 8, "the row histogram fits below the list");
+    unsigned long long *kc = ctab;                                           // per chunk: kept mass
+    double *cf = reinterpret_cast<double *>(ctab + kWideMaxChunks);           // per chunk: mass conversion
+    int *cd = reinterpret_cast<int *>(ctab + 2 * kWideMaxChunks);             // per chunk: bin offset G - G_c
+    static_assert(2 * kWideMaxChunks * 8 + kWideMaxChunks * 4 <= kMaxChunksLds * 4,
+                  "chunk tables fit the combine's count table");
+    constexpr unsigned long long kMassMask = (1ull << kWideCountShift) - 1ull;
+    constexpr double kUnit = (double)(1ull << (40 - kWideMassBits));
+    const float G = floorf(m * kWideCells);
+    for (int i = tid; i < kWideBins; i += kThreads) { hc[i] = 0u; hm[i] = 0ull; }
+    for (int c = tid; c < S; c += kThreads) {
+        const float Gc = floorf(st[c].m * kWideCells);
+        cd[c] = (int)(G - Gc);
+        cf[c] = exp((double)(Gc * (1.f / kWideCells)) - (double)m) * kUnit;
+        kc[c] = 0ull;
+    }
+    __syncthreads();
+    // chunk mass -> row units, rounded to the nearest integer (< 2^54): the two 32-bit
+    // halves are converted separately (exact), cheaper than a 64-bit conversion
+    auto conv = [&](unsigned long long v, int c) -> unsigned long long {
+        const double x = rint((double)(v & kMassMask) * cf[c]);
+        const double hi = floor(x * 2.3283064365386963e-10);   // x / 2^32
+        const double lo = fma(hi, -4294967296.0, x);            // x - hi * 2^32, exact
+        return ((unsigned long long)(uint32_t)hi << 32) | (uint32_t)lo;
+    };
+    // 1. merge: thread t reads words t, t + 256, ... of the row's chunk histograms
+    //    (chunk c = word >> 10), sixteen loads in flight
+    static_assert(kWideBins == 1024, "chunk index = word >> 10");
+    const int nw = S * kWideBins;
+    for (int q0 = 0; q0 < nw; q0 += 16 * kThreads) {
+        unsigned long long v[16];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) v[u] = hist[min(q0 + u * kThreads + tid, nw - 1)];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+            const int q = q0 + u * kThreads + tid;
+            if (q < nw && v[u] != 0ull) {
+                const int c = q >> 10, j = min((q & (kWideBins - 1)) + cd[c], kWideBins - 1);
+                atomicAdd(&hc[j], (uint32_t)(v[u] >> kWideCountShift));
+                atomicAdd(&hm[j], conv(v[u], c));
+            }
+        }
+    }
+    __syncthreads();
+    // 2. the cut bin: wave 0, 16 consecutive bins per lane
+    if (wave_id() == 0) {
+        const int l = lane_id();
+        unsigned long long ws = 0ull;
+        uint32_t cs = 0u;
+#pragma unroll
+        for (int j = 0; j < kWideBins / 64; ++j) { ws += hm[l * (kWideBins / 64) + j]; cs += hc[l * (kWideBins / 64) + j]; }
+        const unsigned long long wi = wave_incl_scan(ws);
+        const uint32_t ci = wave_incl_scan(cs);
+        const unsigned long long total = readlane(wi, 63);
+        const double target = (double)p.top_p * (double)total;
+        const unsigned long long bal = __ballot((double)wi > target);
+        if (l == 0) { ms.flag = 0; ms.da = target; }
+        if (bal != 0ull && l == __ffsll((long long)bal) - 1) {
+            unsigned long long acc = wi - ws;
+            uint32_t nacc = ci - cs;
+            for (int j = 0; j < kWideBins / 64; ++j) {
+                const int b = l * (kWideBins / 64) + j;
+                if ((double)(acc + hm[b]) > target) {
+                    ms.sel_digit = (uint32_t)b;
+                    ms.sel_above_mass = acc;
+                    ms.sel_above_count = nacc;
+                    ms.ib = (int)hc[b];
+                    ms.flag = 1;
+                    break;
+                }
+                acc += hm[b];
+                nacc += hc[b];
+            }
+        }
+    }
+    __syncthreads();
+    const int bstar = (int)ms.sel_digit, nb = ms.ib;
+    const double target = ms.da;
+    if (!ms.flag || bstar == kWideBins - 1 || nb < 1) return false;
+    const unsigned long long above = ms.sel_above_mass;
+    const uint32_t above_count = ms.sel_above_count;
+    // 3. per chunk: the mass of its bins above the cut bin; sixteen loads in flight, the
+    //    256 words of one load round all of one chunk (a wave sum, one LDS atomic)
+    static_assert(kWideBins % kThreads == 0, "a load round stays within one chunk");
+    for (int q0 = 0; q0 < nw; q0 += 16 * kThreads) {
+        unsigned long long v[16];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) v[u] = hist[min(q0 + u * kThreads + tid, nw - 1)];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+            const int qr = q0 + u * kThreads;   // (uniform)
+            if (qr >= nw) break;
+            const int c = qr >> 10, jc = (qr + tid) & (kWideBins - 1);
+            unsigned long long msum = (v[u] != 0ull && jc + cd[c] < bstar) ? conv(v[u], c) : 0ull;
+            msum = wave_reduce(msum, OpSumQ(), 0ull);
+            if (lane_id() == 0 && msum) atomicAdd(&kc[c], msum);
+        }
+    }
+    if (tid == 0) ms.ncand = 0;
+    for (int i = tid; i < 256; i += kThreads) { ms.hist[i] = 0u; ms.hmass[i] = 0ull; }
+    __syncthreads();
+    // 4. the cut bin's entries (scores in [lo_b, hi_b)): one pass over the row's scores,
+    //    sixteen 16-byte loads per thread in flight, the next block requested before the
+    //    current one is tested; split 256 ways by score (sub-bin 0 the highest; equal
+    //    scores share one) and kept in L when the bin fits
+    const float cell = G - (float)bstar;
+    const float lo_b = cell * (1.f / kWideCells), hi_b = (cell + 1.f) * (1.f / kWideCells);
+    const float sscale = 256.f * kWideCells;
+    auto sub = [&](float y) { return min(255, (int)((hi_b - y) * sscale)); };
+    const bool listed = nb <= kWideList;
+    auto each_cut = [&](auto f) {   // f(score, index) over the cut bin's entries
+        constexpr int U = 16;
+        const int n4 = (V + 3) / 4;   // the buffer is readable up to V rounded up to 4
+        const float4 *y4 = reinterpret_cast<const float4 *>(yb);
+        float4 qa[U], qb[U];
+        auto request = [&](float4 (&q)[U], int b0) {
+#pragma unroll
+            for (int u = 0; u < U; ++u) q[u] = y4[min(b0 + u * kThreads + tid, n4 - 1)];
+        };
+        request(qa, 0);
+        for (int b0 = 0; b0 < n4; b0 += U * kThreads) {
+            request(qb, b0 + U * kThreads);
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const float t[4] = {qa[u].x, qa[u].y, qa[u].z, qa[u].w};
+                bool any = false;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) any |= (t[e] >= lo_b) & (t[e] < hi_b);
+                if (any) {
+                    const int i0 = 4 * (b0 + u * kThreads + tid);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        if (t[e] >= lo_b && t[e] < hi_b && i0 + e < V && b0 + u * kThreads + tid < n4) f(t[e], i0 + e);
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < U; ++u) qa[u] = qb[u];
+        }
+    };
+    each_cut([&](float y, int idx) {
+        const int sb = sub(y);
+        atomicAdd(&ms.hist[sb], 1u);
+        atomicAdd(&ms.hmass[sb], weight_fix(y, m));
+        if (listed) {
+            const int pos = wave_append(&ms.ncand);
+            if (pos < kWideList) L[pos] = desc_key(y, idx);
+        }
+    });
+    __syncthreads();
+    if (listed && ms.ncand != nb) return false;   // (the histogram and the scores always agree)
+    if (wave_id() == 0) {
+        const int l = lane_id();
+        unsigned long long c[4], ws = 0ull;
+        uint32_t n[4], ns = 0u;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) { c[j] = ms.hmass[4 * l + j]; n[j] = ms.hist[4 * l + j]; ws += c[j]; ns += n[j]; }
+        const unsigned long long wi = above + wave_incl_scan(ws);
+        const uint32_t ni = above_count + wave_incl_scan(ns);
+        const unsigned long long bal = __ballot((double)wi > target);
+        // no sub-bin crossing (rounding): the last non-empty one is taken
+        const unsigned long long nonempty = __ballot(ns > 0u);
+        const int fl = bal ? __ffsll((long long)bal) - 1 : 63 - __clzll((long long)nonempty);
+        if (l == fl) {
+            // the lane's crossing sub-bin (or its last non-empty one), and the mass and
+            // count above it (static indices only)
+            unsigned long long acc = wi - ws, acc_at = acc;
+            uint32_t nacc = ni - ns, nacc_at = nacc;
+            int js = -1;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const bool take = bal ? (js < 0 && (double)(acc + c[j]) > target) : (n[j] > 0u);
+                if (take) { js = j; acc_at = acc; nacc_at = nacc; }
+                acc += c[j];
+                nacc += n[j];
+            }
+            ms.sel_need = (uint32_t)(4 * l + max(js, 0));
+            ms.sel_above_mass = acc_at;
+            ms.sel_above_count = nacc_at;
+        }
+        if (l == 0) ms.ncand = 0;
+    }
+    __syncthreads();
+    const int sstar = (int)ms.sel_need;
+    const unsigned long long above_s = ms.sel_above_mass;
+    const uint32_t above_count_s = ms.sel_above_count;
+    if (listed) {
+        for (int i = tid; i < nb; i += kThreads) {
+            const unsigned long long k = L[i];
+            if (sub(desc_key_y(k)) == sstar) {
+                const int pos = wave_append(&ms.ncand);
+                if (pos < kWideCross) D[pos] = k;
+            }
+        }
+    } else {
+        // a bin larger than the list: the crossing sub-bin from a second pass
+        each_cut([&](float y, int idx) {
+            if (sub(y) == sstar) {
+                const int pos = wave_append(&ms.ncand);
+                if (pos < kWideCross) D[pos] = desc_key(y, idx);
+            }
+        });
+    }
+    __syncthreads();
+    const int ns = ms.ncand;
+    if (ns > kWideCross) return false;
+    sort_keys(D, ns, ms.part);
+    TopPCut tc;
+    cut_in_sorted(D, ns, above_s, above_count_s, target, m, tc, ms);
+    const float cut = tc.cut;
+    const int cut_idx = tc.cut_idx == 0x7fffffff ? V : tc.cut_idx;
+    const unsigned long long zf = tc.zf;
+    auto kept = [&](float y, int idx) { return y > cut || (y == cut && idx <= cut_idx); };
+    // 5. each chunk's kept cut-bin entries (a third pass over the scores when they were
+    //    not listed)
+    if (listed) {
+        for (int i = tid; i < nb; i += kThreads) {
+            const float y = desc_key_y(L[i]);
+            const int idx = desc_key_idx(L[i]);
+            if (kept(y, idx)) atomicAdd(&kc[idx / C], weight_fix(y, m));
+        }
+    } else {
+        each_cut([&](float y, int idx) {
+            if (kept(y, idx)) atomicAdd(&kc[idx / C], weight_fix(y, m));
+        });
+    }
+    __syncthreads();
+    // the chunk where the kept mass in vocab order crosses u * total
+    const unsigned long long tgt = (unsigned long long)floor((double)p.uniform * (double)zf);
+    if (wave_id() == 0) {
+        const int l = lane_id();
+        unsigned long long run = 0ull, before = 0ull;
+        int cs = -1, clast = -1;
+        for (int c0 = 0; c0 < S && cs < 0; c0 += 64) {
+            const int c = c0 + l;
+            const unsigned long long w = c < S ? kc[c] : 0ull;
+            const unsigned long long incl = run + wave_incl_scan(w);
+            const unsigned long long bal = __ballot(c < S && incl > tgt);
+            const unsigned long long pos = __ballot(w > 0ull);
+            if (pos) clast = c0 + 63 - __clzll((long long)pos);
+            if (bal) {
+                const int fl = __ffsll((long long)bal) - 1;
+                cs = c0 + fl;
+                before = readlane(incl - w, fl);
+            }
+            run = readlane(incl, 63);
+        }
+        if (cs < 0) { cs = clast >= 0 ? clast : 0; before = 0ull; }   // (rounding)
+        if (l == 0) { ms.ia = cs; ms.sel_above_mass = before; }
+    }
+    __syncthreads();
+    const int cs = ms.ia;
+    const unsigned long long rem = tgt - min(tgt, ms.sel_above_mass);
+    __syncthreads();
+    // its scores walked in vocab order (the last kept one if rounding leaves it short)
+    const int c0 = cs * C, cn = min(C, V - c0);
+    const DenseSource ks{yb + c0, cn, cut, cut_idx - c0};
+    int last;
+    int tok = dense_draw(ks, m, rem, ms, last);
+    if (tok < 0) tok = last >= 0 ? last : 0;
+    RowOut r;
+    r.token = c0 + tok;
+    r.m = m;
+    r.cut = cut;
+    r.cut_idx = cut_idx;
+    r.kept = tc.kept;
+    r.log_norm = log((double)zf / kFixScale);
+    r.logprob = (double)yb[r.token] - (double)m - r.log_norm;
+    r.path = 2;
+    write_row(a, row, mode, r, min(want, tc.kept), ms);
+    return true;
+}
+
+// The kept entries of an LDS list of sort keys (for radix selects).
+struct KeptListSource {
+    const unsigned long long *E;
+    int n;
+    float cut;
+    int cut_idx;
+    template <class F>
+    __device__ __forceinline__ void each(F f) const {
+        for (int i = threadIdx.x; i < n; i += kThreads) {
+            const unsigned long long k = E[i];
+            const float y = desc_key_y(k);
+            const int idx = desc_key_idx(k);
+            if (y > cut || (y == cut && idx <= cut_idx)) f(fkey(y), idx, y);
+        }
+    }
+};
+
+// Finish a sampled row from the unsorted list E[0..n) of sort keys (final-space scores),
+// which holds every entry of the row scoring at least its smallest score.  Nothing of
+// size n is sorted: each step is a 256-way histogram over the list and a sort of the
+// crossing part only.
+//  * top-p (`topp`): the cut in exclusive form against p * Z, Z = `zrow` (units of 2^-40
+//    relative to the list's max; the whole row's mass for top-p-only rows) or, for
+//    zrow < 0, the list's own mass (top-k rows);
+//  * the draw: the kept mass in vocab order, over 256 index ranges, then the crossing
+//    range sorted by index and walked;
+//  * top-N: a radix select of the N-th kept score, the kept entries reaching it sorted.
+// `W` is LDS for kSortCap keys, apart from E.  Returns false, writing nothing, when the
+// top-p cut does not fall within E and E is not the whole row (`complete`).
+__device__ __forceinline__ bool finish_list(const Args &a, int row, int mode, const klsample_row_params &p,
+                                            const unsigned long long *E, int n, bool topp, double zrow,
+                                            bool complete, unsigned long long *W, Misc &ms) {
+    const int V = a.V, N = a.N, tid = threadIdx.x;
+    uint32_t kmin = 0xffffffffu, kmax = 0u;
+    for (int i = tid; i < n; i += kThreads) {
+        const uint32_t k = fkey(desc_key_y(E[i]));
+        kmin = min(kmin, k);
+        kmax = max(kmax, k);
+    }
+    kmin = block_reduce(kmin, OpMinU(), ms.red.u, 0xffffffffu);
+    kmax = block_reduce(kmax, OpMaxU(), ms.red.u, 0u);
+    const float ylo = fkey_inv(kmin), yhi = fkey_inv(kmax);
+    const float mref = yhi;
+    TopPCut tc;
+    tc.cut = kNegInf;
+    tc.cut_idx = 0x7fffffff;
+    tc.kept = n;
+    tc.zf = 0ull;
+    bool cut_all = true;   // every entry kept
+    if (topp || zrow < 0.0) {
+        unsigned long long z = 0ull;
+        for (int i = tid; i < n; i += kThreads) z += weight_fix(desc_key_y(E[i]), mref);
+        tc.zf = block_sumq(z, ms);
+    }
+    if (topp) {
+        // 256 score bins over [ylo, yhi], bin 0 the highest (equal scores share a bin)
+        const float span = yhi - ylo;
+        float scale = span > 0.f ? 256.f / span : 0.f;
+        if (!(scale <= __FLT_MAX__)) scale = 0.f;
+        auto bin = [&](float y) { return min(255, (int)((yhi - y) * scale)); };
+        for (int i = tid; i < 256; i += kThreads) { ms.hist[i] = 0u; ms.hmass[i] = 0ull; }
+        __syncthreads();
+        for (int i = tid; i < n; i += kThreads) {
+            const float y = desc_key_y(E[i]);
+            atomicAdd(&ms.hist[bin(y)], 1u);
+            atomicAdd(&ms.hmass[bin(y)], weight_fix(y, mref));
+        }
+        __syncthreads();
+        const double target = (double)p.top_p * (zrow >= 0.0 ? zrow : (double)tc.zf);
+        if (wave_id() == 0) {
+            const int l = lane_id();
+            unsigned long long c[4], ws = 0ull;
+            uint32_t nn[4], ns = 0u;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) { c[j] = ms.hmass[4 * l + j]; nn[j] = ms.hist[4 * l + j]; ws += c[j]; ns += nn[j]; }
+            const unsigned long long wi = wave_incl_scan(ws);
+            const uint32_t ni = wave_incl_scan(ns);
+            const unsigned long long bal = __ballot((double)wi > target);
+            if (l == 0) ms.flag = bal ? 1 : 0;
+            if (bal && l == __ffsll((long long)bal) - 1) {
+                unsigned long long acc = wi - ws, acc_at = acc;
+                uint32_t nacc = ni - ns, nacc_at = nacc;
+                int js = -1;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    if (js < 0 && (double)(acc + c[j]) > target) { js = j; acc_at = acc; nacc_at = nacc; }
+                    acc += c[j];
+                    nacc += nn[j];
+                }
+                ms.sel_need = (uint32_t)(4 * l + max(js, 0));
+                ms.sel_above_mass = acc_at;
+                ms.sel_above_count = nacc_at;
+            }
+            if (l == 0) ms.ncand = 0;
+        }
+        __syncthreads();
+        if (ms.flag) {
+            // the crossing bin, sorted, gives the crossing entry and the ties it keeps
+            const int bs = (int)ms.sel_need;
+            const unsigned long long above = ms.sel_above_mass;
+            const uint32_t above_count = ms.sel_above_count;
+            for (int i = tid; i < n; i += kThreads) {
+                const unsigned long long k = E[i];
+                if (bin(desc_key_y(k)) == bs) W[wave_append(&ms.ncand)] = k;
+            }
+            __syncthreads();
+            const int nb = ms.ncand;
+            sort_keys(W, nb, ms.part);
+            cut_in_sorted(W, nb, above, above_count, target, mref, tc, ms);
+            cut_all = false;
+        } else if (!complete) {
+            return false;   // the kept mass reaches past the list
+        }
+    }
+    // (nothing cut: the list's smallest score, every entry scoring it being listed)
+    const float cut = cut_all ? ylo : tc.cut;
+    const int cut_idx = (cut_all || tc.cut_idx == 0x7fffffff) ? V : tc.cut_idx;
+    const int kept_n = cut_all ? n : tc.kept;
+    const unsigned long long zf = tc.zf;
+    auto kept = [&](float y, int idx) { return y > cut || (y == cut && idx <= cut_idx); };
+    // the draw: kept mass over 256 index ranges, then the crossing range sorted by index
+    const int rw = (V + 255) / 256;
+    for (int i = tid; i < 256; i += kThreads) { ms.hist[i] = 0u; ms.hmass[i] = 0ull; }
+    __syncthreads();
+    for (int i = tid; i < n; i += kThreads) {
+        const float y = desc_key_y(E[i]);
+        const int idx = desc_key_idx(E[i]);
+        if (kept(y, idx)) {
+            atomicAdd(&ms.hist[idx / rw], 1u);
+            atomicAdd(&ms.hmass[idx / rw], weight_fix(y, mref));
+        }
+    }
+    __syncthreads();
+    const unsigned long long tgt = (unsigned long long)floor((double)p.uniform * (double)zf);
+    if (wave_id() == 0) {
+        const int l = lane_id();
+        unsigned long long c[4], ws = 0ull;
+        uint32_t nn[4], ns = 0u;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) { c[j] = ms.hmass[4 * l + j]; nn[j] = ms.hist[4 * l + j]; ws += c[j]; ns += nn[j]; }
+        const unsigned long long wi = wave_incl_scan(ws);
+        const unsigned long long bal = __ballot(wi > tgt);
+        const unsigned long long nonempty = __ballot(ns > 0u);
+        // (no range crossing: rounding; the last kept entry is taken)
+        const int fl = bal ? __ffsll((long long)bal) - 1 : 63 - __clzll((long long)nonempty);
+        if (l == fl) {
+            unsigned long long acc = wi - ws, acc_at = acc;
+            int js = -1;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const bool take = bal ? (js < 0 && acc + c[j] > tgt) : (nn[j] > 0u);
+                if (take) { js = j; acc_at = acc; }
+                acc += c[j];
+            }
+            ms.ib = 4 * l + max(js, 0);
+            ms.sel_above_mass = bal ? acc_at : ~0ull;
+        }
+        if (l == 0) ms.ncand = 0;
+    }
+    __syncthreads();
+    const int rr = ms.ib;
+    const unsigned long long rem = ms.sel_above_mass == ~0ull ? ~0ull : tgt - ms.sel_above_mass;
+    for (int i = tid; i < n; i += kThreads) {
+        const float y = desc_key_y(E[i]);
+        const int idx = desc_key_idx(E[i]);
+        if (kept(y, idx) && idx / rw == rr)
+            W[wave_append(&ms.ncand)] = ((unsigned long long)(uint32_t)idx << 32) | __float_as_uint(y);
+    }
+    __syncthreads();
+    const int nr = ms.ncand;
+    sort_keys(W, nr, ms.part);
+    if (wave_id() == 0) {
+        const int l = lane_id();
+        unsigned long long run = 0ull;
+        int found = -1;
+        for (int i0 = 0; i0 < nr && found < 0; i0 += 64) {
+            const int i = i0 + l;
+            const unsigned long long w = i < nr ? weight_fix(__uint_as_float((uint32_t)W[i]), mref) : 0ull;
+            const unsigned long long incl = run + wave_incl_scan(w);
+            const unsigned long long bal = __ballot(i < nr && incl > rem);
+            if (bal) found = i0 + __ffsll((long long)bal) - 1;
+            run = readlane(incl, 63);
+        }
+        if (found < 0) found = max(nr - 1, 0);
+        if (l == 0) ms.ia = found;
+    }
+    __syncthreads();
+    const unsigned long long kt = W[ms.ia];
+    RowOut r;
+    r.token = (int)(kt >> 32);
+    r.m = mref;
+    r.cut = cut;
+    r.cut_idx = cut_idx;
+    r.kept = kept_n;
+    r.log_norm = log((double)zf / kFixScale);
+    r.logprob = (double)__uint_as_float((uint32_t)kt) - (double)mref - r.log_norm;
+    r.path = 0;
+    // top-N: the N-th kept score by radix select, the kept entries reaching it sorted
+    const int want = min(N, kept_n);
+    __syncthreads();   // (W is read before it is reused)
+    if (want > 0) {
+        const KeptListSource ks{E, n, cut, cut_idx};
+        const uint32_t kn = select_kth(ks, (uint32_t)want, ms);
+        if (tid == 0) ms.ncand = 0;
+        __syncthreads();
+        ks.each([&](uint32_t key, int idx, float y) {
+            if (key >= kn) {
+                const int pos = wave_append(&ms.ncand);
+                if (pos < kSortCap) W[pos] = desc_key(y, idx);
+            }
+        });
+        __syncthreads();
+        const int t = min(ms.ncand, kSortCap);
+        sort_keys(W, t, ms.part);
+        for (int i = tid; i < want; i += kThreads) {
+            ms.topn_idx[i] = desc_key_idx(W[i]);
+            ms.topn_y[i] = desc_key_y(W[i]);
+        }
+        __syncthreads();
+    }
+    write_row(a, row, mode, r, want, ms);
+    return true;
+}
+
 // Resolve one row from its chunk summaries and candidates (or hand it to
 // dense_resolve).  Runs in one workgroup of kThreads.
 // Copy the entries of `src` scoring >= lo into the LDS list `dst` (capacity cap);
@@ -1621,70 +2148,6 @@ __device__ __forceinline__ int gather_keys(const Src &src, float lo, unsigned lo
     });
     __syncthreads();
     return ms.ncand;
-}
-
-// Given D[0..n) sorted best first and the kept prefix length L, finish a sampled
-// row: normaliser, cut, top-N, inverse CDF in vocab order (D is reused as scratch).
-__device__ __forceinline__ void finish_sampled(const Args &a, int row, int mode, const klsample_row_params &p,
-                               unsigned long long *D, int n, int L, double mref, Misc &ms) {
-    const int V = a.V;
-    RowOut r;
-    r.path = 0;
-    double zs = 0.0;
-    for (int i = threadIdx.x; i < L; i += kThreads) zs += exp((double)desc_key_y(D[i]) - mref);
-    const double zf = block_sumd(zs, ms);
-    const float cut_y = desc_key_y(D[L - 1]);
-    const bool partial = (L < n) && (desc_key_y(D[L]) == cut_y);
-    r.m = (float)mref;
-    r.cut = cut_y;
-    r.cut_idx = partial ? desc_key_idx(D[L - 1]) : V;
-    r.kept = L;
-    r.log_norm = log(zf);
-    const int count = min(a.N, L);
-    for (int t = threadIdx.x; t < count; t += kThreads) {
-        ms.topn_idx[t] = desc_key_idx(D[t]);
-        ms.topn_y[t] = desc_key_y(D[t]);
-    }
-    __syncthreads();
-    // the kept set in vocab order, then the first index whose cumulative weight
-    // exceeds u * zf
-    for (int i = threadIdx.x; i < L; i += kThreads) {
-        const unsigned long long k = D[i];
-        D[i] = ((unsigned long long)(uint32_t)desc_key_idx(k) << 32) | __float_as_uint(desc_key_y(k));
-    }
-    __syncthreads();
-    sort_keys(D, L, ms.part);
-    int last;
-    double before;
-    int j = ordered_find(
-        L, [&](int i) { return exp((double)__uint_as_float((uint32_t)D[i]) - mref); },
-        (double)p.uniform * zf, ms, last, before);
-    if (j < 0) j = last >= 0 ? last : 0;
-    r.token = (int)(D[j] >> 32);
-    r.logprob = (double)__uint_as_float((uint32_t)D[j]) - mref - r.log_norm;
-    __syncthreads();
-    write_row(a, row, mode, r, count, ms);
-}
-
-// Length of the kept prefix of D[0..n) (sorted best first) under top-p: the first i
-// whose exclusive mass exceeds p * zref (the crossing entry is kept), or -1 if no
-// entry of D crosses.
-__device__ __forceinline__ int topp_prefix(const unsigned long long *D, int n, double mref, double zref, float top_p, Misc &ms) {
-    const int seg = (n + kThreads - 1) / kThreads;
-    const int i0 = min((int)threadIdx.x * seg, n), i1 = min(i0 + seg, n);
-    double s = 0.0;
-    for (int i = i0; i < i1; ++i) s += exp((double)desc_key_y(D[i]) - mref);
-    double tot;
-    const double ex = block_excl_scan(s, ms.red.d, tot);
-    const double target = (double)top_p * zref;
-    int cut = 0x7fffffff;
-    double c = ex;
-    for (int i = i0; i < i1; ++i) {
-        if (cut == 0x7fffffff && c > target) cut = i;
-        c += exp((double)desc_key_y(D[i]) - mref);
-    }
-    cut = block_min(cut, ms);
-    return cut == 0x7fffffff ? -1 : cut;
 }
 
 // ---------------------------------------------------------------------------------
@@ -1765,7 +2228,7 @@ __device__ __forceinline__ void wave_write(const Args &a, int row, int mode, con
 
 // Finish a sampled row in one wave: D[0..n) sorted best first, the first L kept
 // (1 <= L <= 64, L <= n), N <= 64; `scr` is 128 free LDS words of 8 bytes.  Same
-// results as finish_sampled.  The draw ranks the kept entries by vocab index (broadcast
+// results as finish_list.  The draw ranks the kept entries by vocab index (broadcast
 // LDS reads, or `irank`), places their weights in index order and takes one prefix scan.
 // `wz`, when given, holds the lane's weight exp(y - mref) and the kept entries' sum.
 __device__ __forceinline__ void wave_finish(const Args &a, int row, int mode, const klsample_row_params &p,
@@ -2093,7 +2556,7 @@ __device__ __forceinline__ bool combine_row(const Args &a, int row, const klsamp
     float m = kNegInf, lo = kNegInf;
     int nfinite = 0, ovf = 0;
     if (has) {
-        m = s0.m; lo = s0.y_thr; nfinite = s0.nfinite; ovf = s0.overflow;
+        m = s0.m; lo = s0.y_thr; nfinite = s0.nfinite; ovf = s0.flags & kChunkOverflow;
         const int nc = min(s0.ncand, a.cand_cap);
         cnt[tid] = nc;
         if (tid >= nspec ? nc > 0 : nc > 2 * ppc) ovf |= 2;
@@ -2103,7 +2566,7 @@ __device__ __forceinline__ bool combine_row(const Args &a, int row, const klsamp
         m = fmaxf(m, s.m);
         lo = fmaxf(lo, s.y_thr);
         nfinite += s.nfinite;
-        ovf |= s.overflow;
+        ovf |= s.flags & kChunkOverflow;
         const int nc = min(s.ncand, a.cand_cap);
         cnt[c] = nc;
         if (c >= nspec ? nc > 0 : nc > 2 * ppc) ovf |= 2;
@@ -2475,48 +2938,41 @@ __device__ __forceinline__ bool combine_row(const Args &a, int row, const klsamp
         if (lk < 0) {
             float xt = kNegInf;
             if (nF > kk) {
-                if (best(kk) < 0) return false;
-                xt = quotient_threshold(__fdiv_rn(desc_key_y(D[kk - 1]), p.temperature), p.temperature);
+                // the kk-th largest score by radix select: the top set is every candidate
+                // whose quotient reaches its quotient
+                const float xk = fkey_inv(select_kth(LdsSource{A, nF}, (uint32_t)kk, ms));
+                xt = quotient_threshold(__fdiv_rn(xk, p.temperature), p.temperature);
             }
             lk = gather_ge(A, nF, xt, D, kSortCap, ms);
             if (lk > kSortCap) return false;
         }
+        const bool topp = (p.flags & KLSAMPLE_ROW_TOP_P) != 0;
+        const bool small = lk <= 64 && N <= 64;
         if (lk_pre < 0 || p.temperature != 1.f) {
-            // divided and sorted in final space (a gather already sorted at T = 1 stays)
+            // divided into final space; sorted when the one-wave finish takes it (a
+            // gather already sorted at T = 1 stays)
             for (int i = tid; i < lk; i += kThreads) {
                 const unsigned long long k = D[i];
                 D[i] = desc_key(__fdiv_rn(desc_key_y(k), p.temperature), desc_key_idx(k));
             }
             __syncthreads();
-            sort_top(D, lk, ms);
+            if (small) sort_top(D, lk, ms);
         }
+        if (!small) return finish_list(a, row, mode, p, D, lk, topp, -1.0, true, A, ms);
         const double mref = (double)desc_key_y(D[0]);
-        const bool topp = (p.flags & KLSAMPLE_ROW_TOP_P) != 0;
-        if (lk <= 64 && N <= 64) {
-            if (wave_id() == 0) {
-                int L = lk;
-                if (topp) {
-                    const double w = lane_id() < lk ? (double)__expf(desc_key_y(D[lane_id()]) - (float)mref) : 0.0;
-                    const int cut = wave_topp(D, lk, mref, wave_reduce(w, OpSumD(), 0.0), p.top_p);
-                    if (cut > 0) L = cut;
-                }
-                wave_finish(a, row, mode, p, D, lk, L, mref, A);
+        if (wave_id() == 0) {
+            int L = lk;
+            if (topp) {
+                const double w = lane_id() < lk ? (double)__expf(desc_key_y(D[lane_id()]) - (float)mref) : 0.0;
+                const int cut = wave_topp(D, lk, mref, wave_reduce(w, OpSumD(), 0.0), p.top_p);
+                if (cut > 0) L = cut;
             }
-            return true;
+            wave_finish(a, row, mode, p, D, lk, L, mref, A);
         }
-        int L = lk;
-        if (topp) {
-            double zs = 0.0;
-            for (int i = tid; i < lk; i += kThreads) zs += exp((double)desc_key_y(D[i]) - mref);
-            const double zk = block_sumd(zs, ms);
-            const int cut = topp_prefix(D, lk, mref, zk, p.top_p, ms);
-            if (cut > 0) L = cut;
-        }
-        finish_sampled(a, row, mode, p, D, lk, L, mref, ms);
         return true;
     }
 
-    // top-p alone: the best 64 (one wave), then the best 256, then every candidate
+    // top-p alone: the best 48 or 64 (one wave), else every candidate (finish_list)
     const double mref = (double)m;
     if (nF > 64 && N <= 64) {
         // First the best 48 (and the ties of their bin): when that is at most 64 entries
@@ -2560,37 +3016,28 @@ __device__ __forceinline__ bool combine_row(const Args &a, int row, const klsamp
             }
         }
     }
-    int n = 0, L = -1;
-    for (int R = 64;; R = (R < kThreads) ? kThreads : nF) {
-        if (R > nF) R = nF;
-        n = best(R);
-        if (n < 0) return false;
-        if (n <= 64) {
-            if (wave_id() == 0) {
-                const int cut = wave_topp(D, n, mref, Z, p.top_p);
-                if (lane_id() == 0) ms.flag = cut;
-            }
-            __syncthreads();
-            L = ms.flag;
-        } else {
-            L = topp_prefix(D, n, mref, Z, p.top_p, ms);
-        }
-        if (L > 0 || R >= nF) break;
+    if (nF > 64 || N > 64) {
+        // a kept set past the best 64 (or a long top-N list): from the unsorted candidates
+        // (the kept set must lie within them unless they are the whole row)
+        return finish_list(a, row, mode, p, A, nF, true, Z * kFixScale, !(lo > kNegInf), D, ms);
     }
+    const int n = best(nF);
+    if (n < 0) return false;
+    if (wave_id() == 0) {
+        const int cut = wave_topp(D, n, mref, Z, p.top_p);
+        if (lane_id() == 0) ms.flag = cut;
+    }
+    __syncthreads();
+    int L = ms.flag;
     if (L < 0) {
         if (lo > kNegInf) return false;   // the kept mass reaches past the candidates
         L = n;                            // the candidates are the whole row
     }
-    if (L <= 64 && N <= 64) {
-        if (wave_id() == 0) wave_finish(a, row, mode, p, D, n, L, mref, A);
-        return true;
-    }
-    finish_sampled(a, row, mode, p, D, n, L, mref, ms);
+    if (wave_id() == 0) wave_finish(a, row, mode, p, D, n, L, mref, A);
     return true;
 }
 
-__device__ __forceinline__ void map_block(const Args &a, int &row, int &chunk) {
-    const int w = blockIdx.x;
+__device__ __forceinline__ void map_block(const Args &a, int w, int &row, int &chunk) {
     if (a.xcd_map) {
         // consecutive workgroup ids go to consecutive XCDs: keep a row's chunks on one
         // XCD so the row's history is fetched into one L2
@@ -2618,8 +3065,62 @@ struct ScanLds {
     static constexpr int mask_off = stage_off + kWaves * kStageLanes * stride * 4;
     static constexpr int penalty = mask_off + kThreads * 4;
     static constexpr int keys = kThreads * (E < 16 ? E : 16) * 4;   // fallback bound (later)
-    static constexpr int value = penalty > keys ? penalty : keys;
+    static constexpr int wide = kWideBins * 8;                       // top-p chunk histogram (last)
+    static constexpr int value0 = penalty > keys ? penalty : keys;
+    static constexpr int value = value0 > wide ? value0 : wide;
 };
+
+// A top-p chunk's histogram and final scores, into the workspace.  Bin j = G -
+// floor(y * kWideCells) with G = floor(mc * kWideCells), capped at the last bin (see
+// internal.h); each histogram word adds 1 at bit kWideCountShift and the entry's weight
+// exp(y - G / kWideCells) in units of 2^-kWideMassBits below it (integer sums: exact
+// and independent of their order).  The scores go to the row's score buffer in vocab
+// order (16-byte stores).  x holds the chunk's final scores, -inf past its end.  `raw`
+// holds kWideBins * 8 bytes of free LDS.
+template <typename TIn, int E>
+__device__ __forceinline__ void wide_chunk(const Args &a, int row, int chunk, const float (&x)[E], float mc,
+                                           unsigned char *raw) {
+    constexpr int VW = Loader<TIn>::VW;
+    constexpr int NV = E / VW;
+    constexpr int C = kThreads * E;
+    static_assert(C <= (1 << (64 - kWideCountShift - 1)), "bin counts must fit above kWideCountShift");
+    static_assert(kWideCountShift >= kWideMassBits + 14, "bin masses must stay below kWideCountShift");
+    const int tid = threadIdx.x;
+    const int c0 = chunk * C, cn = min(C, a.V - c0);
+    unsigned long long *hb = reinterpret_cast<unsigned long long *>(raw);
+    uint4 *h4 = reinterpret_cast<uint4 *>(raw);
+    for (int i = tid; i < kWideBins / 2; i += kThreads) h4[i] = make_uint4(0u, 0u, 0u, 0u);
+    float *yb = a.ybuf + (size_t)row * a.ypitch + c0;
+#pragma unroll
+    for (int v = 0; v < NV; ++v) {
+        const int li = (v * kThreads + tid) * VW;
+        if (li + VW <= cn) {
+#pragma unroll
+            for (int q = 0; q < VW; q += 4)
+                *reinterpret_cast<float4 *>(yb + li + q) =
+                    make_float4(x[v * VW + q], x[v * VW + q + 1], x[v * VW + q + 2], x[v * VW + q + 3]);
+        } else {
+#pragma unroll
+            for (int e = 0; e < VW; ++e)
+                if (li + e < cn) yb[li + e] = x[v * VW + e];
+        }
+    }
+    __syncthreads();   // bins cleared
+    const float G = floorf(mc * kWideCells);
+    const float anchor = G * (1.f / kWideCells);
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+        const float y = x[e];
+        if (y > kNegInf) {
+            const float d = G - floorf(y * kWideCells);
+            const int j = d < (float)(kWideBins - 1) ? (int)d : kWideBins - 1;
+            atomicAdd(&hb[j], (1ull << kWideCountShift) + weight_fix<kWideMassBits>(y, anchor));
+        }
+    }
+    __syncthreads();
+    uint4 *gh = reinterpret_cast<uint4 *>(a.hist + ((size_t)row * a.S + chunk) * kWideBins);
+    for (int i = tid; i < kWideBins / 2; i += kThreads) gh[i] = h4[i];
+}
 
 // Streaming pass: one workgroup per (row, chunk).  The LDS footprint (~26 KB at 32
 // elements per thread) lets six workgroups share a CU, and the register budget is
@@ -2633,7 +3134,8 @@ struct ScanLds {
 // dense work that follows (bound, candidates, sums) sees final scores everywhere
 // with no per-element branch.
 template <typename TIn, int E, bool kVec>
-__device__ __forceinline__ void scan_chunk(const Args &a, int row, int chunk, unsigned char *raw, ScanMisc &ms) {
+__device__ __forceinline__ void scan_chunk(const Args &a, int row, int chunk, unsigned char *raw, ScanMisc &ms,
+                                           bool wide_only) {
     constexpr int VW = Loader<TIn>::VW;
     constexpr int NV = E / VW;
     constexpr int C = kThreads * E;
@@ -2641,6 +3143,8 @@ __device__ __forceinline__ void scan_chunk(const Args &a, int row, int chunk, un
     const int V = a.V;
     const int tid = threadIdx.x;
     const int mode = row_mode(p, V);
+    // a second workgroup of a top-p chunk (small grids): only the histogram and scores
+    if (wide_only && (mode != kTopP || a.S > kWideMaxChunks)) return;
     const bool divided = (mode == kTopP || mode == kFull);   // scores stream in final space
     const int c0 = chunk * C;
     const int cn = min(C, V - c0);
@@ -2825,6 +3329,20 @@ __device__ __forceinline__ void scan_chunk(const Args &a, int row, int chunk, un
 #pragma unroll
         for (int e = 0; e < E; ++e) x[e] = __fdiv_rn(x[e], p.temperature);
     }
+    if (wide_only) {
+        // the chunk max as the first workgroup takes it (wave maxima, then the largest)
+        float mt = kNegInf;
+#pragma unroll
+        for (int e = 0; e < E; ++e) mt = fmaxf(mt, x[e]);
+        const float mw = wave_reduce(mt, OpMaxF(), kNegInf);
+        if (lane_id() == 0) ms.wm[wave_id()] = mw;
+        __syncthreads();
+        float mc = ms.wm[0];
+#pragma unroll
+        for (int w = 1; w < kWaves; ++w) mc = fmaxf(mc, ms.wm[w]);
+        if (mc > kNegInf && fabsf(mc) < kWideMaxScore) wide_chunk<TIn, E>(a, row, chunk, x, mc, raw);
+        return;
+    }
 
     ChunkStat st;
     st.m = kNegInf;
@@ -2832,7 +3350,7 @@ __device__ __forceinline__ void scan_chunk(const Args &a, int row, int chunk, un
     st.y_thr = kNegInf;
     st.ncand = 0;
     st.z = 0.0;
-    st.overflow = 0;
+    st.flags = 0;
     st.nfinite = 0;
     if (mode != kTopK) {
         // per wave (no barrier): max, lowest argmax, sum of exp relative to the wave's
@@ -2873,35 +3391,55 @@ __device__ __forceinline__ void scan_chunk(const Args &a, int row, int chunk, un
 
     const int K = (mode == kGreedy || mode == kFull) ? a.N
                   : (mode == kTopK ? p.top_k : max(kTopPCandidates, a.N));
+    bool wide = false;      // a wide top-p chunk (decided below)
+    float mc = kNegInf;     // ... and its max
     if (K > 0) {
         float bound = kNegInf;
         if (K < cn) bound = chunk_bound<E>(x, K, cn, tab, ms);
         else __syncthreads();
         // candidates: elements >= thr; a finite threshold also excludes -inf scores
         float thr = -__FLT_MAX__;
-        if (bound > kNegInf) {
-            thr = bound;
-            if (mode == kTopK) {
-                // widen by 8 ulps so every element whose quotient by T rounds to at
-                // least bound / T is kept
-                const float d = fmaxf(fabsf(bound) * 9.5367431640625e-07f, p.temperature * 7.174648137343064e-43f);
-                thr = bound - d;
+        auto set_bound = [&](float b) {
+            thr = -__FLT_MAX__;
+            if (b > kNegInf) {
+                thr = b;
+                if (mode == kTopK) {
+                    // widen by 8 ulps so every element whose quotient by T rounds to at
+                    // least b / T is kept
+                    const float d = fmaxf(fabsf(b) * 9.5367431640625e-07f, p.temperature * 7.174648137343064e-43f);
+                    thr = b - d;
+                }
             }
-        }
-        st.y_thr = (mode == kTopK) ? (bound > kNegInf ? __fdiv_rn(bound, p.temperature) : kNegInf) : bound;
-        int my = 0;
+            st.y_thr = (mode == kTopK) ? (b > kNegInf ? __fdiv_rn(b, p.temperature) : kNegInf) : b;
+        };
+        set_bound(bound);
+        // each wave reserves its run of slots (one LDS atomic); the total is known after
+        // the barrier, before any store, so no barrier waits for the stores
+        int my, pos, total;
+        auto reserve = [&]() {
+            my = 0;
 #pragma unroll
-        for (int e = 0; e < E; ++e) my += (x[e] >= thr) ? 1 : 0;
-        const int incl = wave_incl_scan(my);
-        const int wtot = readlane(incl, 63);
-        int wbase = 0;
-        if (lane_id() == 0 && wtot > 0) wbase = atomicAdd(&ms.ncand, wtot);
-        wbase = readlane(wbase, 0);
-        int pos = wbase + incl - my;
-        // every wave has reserved its run: the total is known before any store, so no
-        // barrier waits for the stores
-        __syncthreads();
-        const int total = ms.ncand;
+            for (int e = 0; e < E; ++e) my += (x[e] >= thr) ? 1 : 0;
+            const int incl = wave_incl_scan(my);
+            const int wtot = readlane(incl, 63);
+            int wbase = 0;
+            if (lane_id() == 0 && wtot > 0) wbase = atomicAdd(&ms.ncand, wtot);
+            wbase = readlane(wbase, 0);
+            pos = wbase + incl - my;
+            __syncthreads();
+            total = ms.ncand;
+        };
+        reserve();
+        if (total > a.cand_cap && K < cn) {
+            // Too many for the slots: a wave with few finite elements (the short last
+            // chunk) drags the per-wave bound down.  Once more with the block-wide bound
+            // over the chunk's finest groups.
+            __syncthreads();   // every thread has read the count
+            if (tid == 0) ms.ncand = 0;
+            const float b2 = block_group_bound_dispatch<E>(x, E < 16 ? E : 16, K, tab, ms);
+            if (b2 > bound) set_bound(b2);
+            reserve();
+        }
         // scores are written as streamed: top-k rows in the penalised space (the row
         // kernel divides by T), the others in final space
         // the chunk's slots as a buffer resource: stores past the capacity are dropped by
@@ -2923,7 +3461,18 @@ __device__ __forceinline__ void scan_chunk(const Args &a, int row, int chunk, un
             }
         }
         st.ncand = min(total, a.cand_cap);
-        st.overflow = total > a.cand_cap ? 1 : 0;
+        st.flags = total > a.cand_cap ? kChunkOverflow : 0;
+        // Every chunk of a top-p row also writes its histogram and final scores (at the
+        // end, or in a second workgroup on small grids), so that a row whose kept set
+        // reaches past the candidates can be resolved from them (wide_resolve).  Every
+        // thread takes the same decision.
+        if (mode == kTopP && a.S <= kWideMaxChunks) {
+            mc = ms.wm[0];
+#pragma unroll
+            for (int w = 1; w < kWaves; ++w) mc = fmaxf(mc, ms.wm[w]);
+            wide = mc > kNegInf && fabsf(mc) < kWideMaxScore;
+            if (wide) st.flags |= kChunkWide;
+        }
     } else {
         __syncthreads();
     }
@@ -2947,23 +3496,86 @@ __device__ __forceinline__ void scan_chunk(const Args &a, int row, int chunk, un
         }
         a.stats[(size_t)row * a.S + chunk] = st;
     }
+    if (wide && !a.wide_split) wide_chunk<TIn, E>(a, row, chunk, x, mc, raw);
 }
 
 template <typename TIn, int E, bool kVec>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(E >= 32 ? 6 : E >= 16 ? 7 : 8))) void scan_kernel(Args a) {
     __shared__ __attribute__((aligned(16))) unsigned char raw[ScanLds<E>::value];
     __shared__ ScanMisc ms;
+    // blocks past B * S are the second workgroups of top-p chunks (a.wide_split)
+    const bool wide_only = blockIdx.x >= (unsigned)(a.B * a.S);
     int row, chunk;
-    map_block(a, row, chunk);
-    scan_chunk<TIn, E, kVec>(a, row, chunk, raw, ms);
+    map_block(a, wide_only ? (int)blockIdx.x - a.B * a.S : (int)blockIdx.x, row, chunk);
+    scan_chunk<TIn, E, kVec>(a, row, chunk, raw, ms, wide_only);
 }
 
 template <int C>
 struct RowLds {
     static constexpr int a = C * 4;
     static constexpr int b = 2 * kSortCap * 8;
-    static constexpr int value = a > b ? a : b;
+    static constexpr int w = (kWideCross + kWideList) * 8;   // wide_resolve
+    static constexpr int ab = a > b ? a : b;
+    static constexpr int value = ab > w ? ab : w;
 };
+
+// Whether every chunk of the row wrote its histogram (and none overflowed its candidate
+// slots).
+__device__ __forceinline__ bool all_chunks_wide(const Args &a, int row, Misc &ms) {
+    int b = 0;
+    for (int c = threadIdx.x; c < a.S; c += kThreads) {
+        const int32_t f = a.stats[(size_t)row * a.S + c].flags;
+        b |= ((f & kChunkWide) == 0 || (f & kChunkOverflow) != 0) ? 1 : 0;
+    }
+    return block_or(b, ms) == 0;
+}
+
+// A row of wide top-p chunks: its max from the chunk summaries, its top-N list from the
+// candidates (every entry of the top N scores at least the largest chunk bound), then
+// wide_resolve.  Returns false if the row is left to dense_resolve.
+__device__ __forceinline__ bool wide_row(const Args &a, int row, const klsample_row_params &p, int mode, unsigned char *raw, int *cnt,
+                         Misc &ms) {
+    const int S = a.S, N = a.N, tid = threadIdx.x;
+    const ChunkStat *st = a.stats + (size_t)row * S;
+    float m = kNegInf, lo = kNegInf;
+    for (int c = tid; c < S; c += kThreads) {
+        const ChunkStat sc = st[c];
+        m = fmaxf(m, sc.m);
+        lo = fmaxf(lo, sc.y_thr);
+        cnt[c] = min(sc.ncand, a.cand_cap);
+    }
+    m = block_max(m, ms);
+    lo = block_max(lo, ms);
+    if (!(m > kNegInf)) return false;
+    int want = 0;
+    if (N > 0) {
+        unsigned long long *A = reinterpret_cast<unsigned long long *>(raw);
+        unsigned long long *D = A + kSortCap;
+        const CandSource src{a.cands + (size_t)row * S * a.cand_cap, cnt, S, a.cand_cap, lo};
+        __syncthreads();   // (the counts in cnt)
+        const int nF = gather_keys(src, lo, A, kSortCap, ms);
+        if (nF < 1) return false;
+        want = min(N, nF);
+        int t;
+        if (nF <= kSortCap) {
+            const LdsSource ls{A, nF};
+            const float tau = fkey_inv(select_kth(ls, (uint32_t)want, ms));
+            t = gather_keys(ls, tau, D, kSortCap, ms);
+        } else {
+            // more candidates than the list holds: the radix select over their slots
+            const float tau = fkey_inv(select_kth(src, (uint32_t)want, ms));
+            t = gather_keys(src, tau, D, kSortCap, ms);
+            if (t > kSortCap) return false;
+        }
+        sort_keys(D, t, ms.part);
+        for (int i = tid; i < want; i += kThreads) {
+            ms.topn_idx[i] = desc_key_idx(D[i]);
+            ms.topn_y[i] = desc_key_y(D[i]);
+        }
+    }
+    __syncthreads();   // (the candidate counts in cnt are no longer needed)
+    return wide_resolve(a, row, p, mode, m, want, raw, reinterpret_cast<unsigned long long *>(cnt), ms);
+}
 
 // One row in one workgroup: combine the chunk candidates, or run the multi-pass path.
 // `raw` holds RowLds<C>::value bytes, `cnt` kMaxChunksLds ints.
@@ -2975,8 +3587,16 @@ __device__ __forceinline__ void row_body(const Args &a, int row, unsigned char *
     request_row(a, row, rs);
     const klsample_row_params p = load_params_vmem(a.params, row);
     const int mode = row_mode(p, a.V);
-    if ((a.options & KLSAMPLE_OPT_FORCE_DENSE) || a.S > kMaxChunksLds ||
-        !combine_row<TIn, E>(a, row, p, mode, rs, raw, cnt, ms)) {
+    const bool force = (a.options & KLSAMPLE_OPT_FORCE_DENSE) != 0;
+    bool done = false;
+    if (!force && a.S <= kMaxChunksLds) done = combine_row<TIn, E>(a, row, p, mode, rs, raw, cnt, ms);
+    if (!done && mode == kTopP && !force && a.S <= kWideMaxChunks) {
+        // a top-p row whose kept set reaches past the candidates: resolved chunk by
+        // chunk from the histograms and scores its chunks wrote
+        __syncthreads();   // the combine's LDS is reused
+        if (all_chunks_wide(a, row, ms)) done = wide_row(a, row, p, mode, raw, cnt, ms);
+    }
+    if (!done) {
         __syncthreads();   // the combine's LDS (cnt included) is reused
         dense_resolve<TIn, E>(a, row, p, mode, raw, cnt, ms);
     }
@@ -2997,7 +3617,7 @@ __global__ __launch_bounds__(kThreads) void probs_kernel(Args a) {
     constexpr int C = kThreads * E;
     __shared__ __attribute__((aligned(16))) uint32_t cnt[C];
     int row, chunk;
-    map_block(a, row, chunk);
+    map_block(a, blockIdx.x, row, chunk);
     const klsample_row_params p = a.params[row];
     const int mode = row_mode(p, a.V);
     const klsample_row_info ri = a.rows[row];
@@ -3030,13 +3650,14 @@ hipError_t mark(const PhaseEvents *ph, int i, hipStream_t s) {
 template <typename TIn, int E>
 hipError_t launch_typed(const Args &a, hipStream_t s, const PhaseEvents *ph) {
     const dim3 grid((unsigned)((int64_t)a.B * a.S));
+    const dim3 scan_grid((unsigned)((int64_t)a.B * a.S * (a.wide_split ? 2 : 1)));
     hipError_t e = mark(ph, 0, s);
     if (e != hipSuccess) return e;
     // 16-byte loads need aligned rows and a last chunk of at least one vector
     const int tail = a.V - (a.S - 1) * a.C;
     const bool vec = a.vec_ok && tail * (int)sizeof(TIn) >= 16;
-    if (vec) scan_kernel<TIn, E, true><<<grid, kThreads, 0, s>>>(a);
-    else scan_kernel<TIn, E, false><<<grid, kThreads, 0, s>>>(a);
+    if (vec) scan_kernel<TIn, E, true><<<scan_grid, kThreads, 0, s>>>(a);
+    else scan_kernel<TIn, E, false><<<scan_grid, kThreads, 0, s>>>(a);
     if ((e = mark(ph, 1, s)) != hipSuccess) return e;
     row_kernel<TIn, E><<<dim3((unsigned)a.B), kThreads, 0, s>>>(a);
     if ((e = mark(ph, 2, s)) != hipSuccess) return e;

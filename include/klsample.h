@@ -74,7 +74,8 @@ typedef struct klsample_row_info {
     int32_t cut_index;
     int32_t kept;
     double log_norm;
-    int32_t path;               /* 0: resolved from chunk candidates, 1: multi-pass row path */
+    int32_t path;               /* 0: resolved from chunk candidates, 1: multi-pass row path,
+                                   2: top-p resolved from the chunks' histograms and scores */
     int32_t mode;               /* 0 greedy, 1 top-k, 2 top-p only, 3 full distribution */
 } klsample_row_info;
 

@@ -233,6 +233,46 @@ def test_wide_vocab_top_p_rows_narrow_their_candidates(n):
     check(out, rows, params, probs=True)
 
 
+@pytest.mark.parametrize('vocab', [151936, 100003, 20001, 600001])
+@pytest.mark.parametrize('dtype', [torch.float32, torch.bfloat16])
+def test_wide_top_p_rows(vocab, dtype):
+    """Flat top-p rows whose kept set reaches far past the chunk candidates (thousands to
+    most of the vocabulary) are resolved chunk by chunk from the chunks' histograms and
+    final scores (row path 2), next to greedy, top-k and heavy-head rows of the same
+    batch; value ties on a coarse grid put many equal scores into the cut."""
+    say(f'wide top-p vocab={vocab} dtype={dtype}')
+    rng = np.random.default_rng(vocab % 1000 + (7 if dtype == torch.bfloat16 else 0))
+    specs = [(1.0, 0.9, 'flat'), (1.4, 0.97, 'flat'), (0.8, 0.8, 'flat'), (1.2, 0.999, 'flat'),
+             (1.0, 0.95, 'grid'), (0.9, 0.9, 'grid8'), (0.7, 0.95, 'heavy'), (0.0, 1.0, 'flat'),
+             (0.9, 0.9, 'topk'), (2.0, 0.5, 'flat')]
+    x = (rng.standard_normal((len(specs), vocab)) * 2.5).astype(np.float32)
+    params, hist = [], []
+    for b, (t, tp, kind) in enumerate(specs):
+        if kind == 'grid':
+            x[b] = np.round(x[b] * 4) / 4          # ties: one score per 1/4
+        elif kind == 'grid8':
+            x[b] = np.round(x[b] * 64) / 64        # ties a little finer than the bins
+        elif kind == 'heavy':
+            x[b, rng.choice(vocab, 100, replace=False)] += 9.0
+        k = 40 if kind == 'topk' else 0
+        params.append(SamplingParams(temperature=t, top_k=k, top_p=tp, repetition_penalty=1.1,
+                                     logprobs=int(rng.choice([0, 5, 64])), presence_penalty=0.3,
+                                     frequency_penalty=0.2))
+        hist.append(rng.integers(0, vocab, int(rng.integers(0, 3000))).tolist())
+    logits = torch.from_numpy(x).to(dtype)
+    u = rng.random(len(specs)).astype(np.float32)
+    u[3] = 0.99999     # a draw near the end of the kept mass
+    rows = sample_rows(logits, hist, params, u)
+    out = run(logits, params, hist, u, probs=True)
+    check(out, rows, params, probs=True)
+    # the flat top-p rows never take the single-workgroup row path (1): the candidates
+    # settle them (0) or the chunk histograms do (2), which the longer rows need
+    paths = out.info['path'].tolist()
+    assert all(paths[b] in (0, 2) for b in (0, 1, 2, 3, 9)), paths
+    if vocab >= 100003:
+        assert all(paths[b] == 2 for b in (0, 1, 3)), paths
+
+
 def test_massive_ties_take_the_row_path():
     say('ties: constant rows')
     V = 50000
