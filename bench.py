@@ -15,7 +15,10 @@ Printed on one JSON line:
   ``klsample_set_phase_events``), against the 8 TB/s HBM peak; ``traffic`` is the
   kernel's measured HBM bytes per launch from the committed rocprofv3 counter summary
   (``profiles/traffic_scan_kernel_f32_b256_v151936.txt``), or null when absent;
-* ``b1_latency_us``: device time per call at B=1, V=151936 bf16 (sampled and greedy),
+  ``whole_call_frac`` is the same bytes over the whole call's device time (both kernels
+  and the gaps between calls);
+* ``b1_latency_us``: device time per call at B=1, V=151936 bf16 (sampled and greedy:
+  the mean of 1000 back-to-back calls, and the median and largest of 100 groups of 10),
   and the host wall time of one ``Sampler.sample`` call;
 * ``cpu_baseline``: the CPU restatement of ``serving/sampling.py:44-63`` in its
   faithful mode (``torch.multinomial`` draw), one call per row as
@@ -26,7 +29,8 @@ Other modes (used to produce the text summaries under ``profiles/``):
 * ``--profile-run``: only the headline steps and a 1 GiB copy that calibrates HBM
   byte counters; meant to run under ``rocprofv3 --pmc``;
 * ``--summarize-stats DIR`` / ``--summarize-pmc FETCH_DIR WRITE_DIR``: turn the CSV
-  output of rocprofv3 into those summaries.
+  output of rocprofv3 into those summaries;
+* ``--summarize-parity JSONL``: the per-case parity counts the GPU tests log.
 """
 from __future__ import annotations
 
@@ -184,6 +188,27 @@ def timed_steps(res, steps, warmup):
     dev_ms = hip.elapsed_ms(e0, e1)
     hip.destroy([e0, e1])
     return wall * 1e3 / steps, dev_ms / steps
+
+
+def per_call_us(res, groups, per_group, warmup):
+    """Device time per call (µs) of ``groups`` groups of ``per_group`` back-to-back calls:
+    HIP events recorded on the launch stream between the groups (a marker between every
+    call would add its own cost to each).  Returns the sorted per-group averages."""
+    import torch
+    for i in range(warmup):
+        res.launch(i)
+    hip = HipEvents()
+    evs = hip.create(groups + 1)
+    torch.cuda.synchronize()
+    hip.record(evs[0], res.stream)
+    for g in range(groups):
+        for i in range(per_group):
+            res.launch(g * per_group + i)
+        hip.record(evs[g + 1], res.stream)
+    torch.cuda.synchronize()
+    out = sorted(hip.elapsed_ms(evs[g], evs[g + 1]) * 1e3 / per_group for g in range(groups))
+    hip.destroy(evs)
+    return out
 
 
 def phase_times(res, steps):
@@ -412,6 +437,35 @@ def summarize_pmc(fetch_root, write_root, command_fetch, command_write):
 
 # ---- main ------------------------------------------------------------------------------------
 
+def summarize_parity(path, command):
+    """The parity counts the GPU tests log (one JSON line per comparison, written when
+    KLSAMPLE_PARITY_LOG names a file) as a table per case."""
+    rows = [json.loads(line) for line in Path(path).read_text().splitlines() if line.strip()]
+    cols = ('rows', 'greedy', 'sampled', 'exact', 'tie_rows', 'margin_rows', 'cdf_rows', 'kept_differs',
+            'boundary_mismatches', 'probs_rows', 'max_prob_rel', 'max_logprob_err', 'failures')
+    agg = {}
+    for r in rows:
+        case = 'golden reference vectors' if r['case'].startswith('golden ') else r['case']
+        a = agg.setdefault(case, dict.fromkeys(cols, 0))
+        for c in cols:
+            a[c] = max(a[c], r[c]) if c.startswith('max_') else a[c] + r[c]
+    lines = ['# Parity counts of the GPU tests against the oracle', '', f'command: `{command}`', '',
+             '* `exact`: rows whose token id equals the oracle\'s (stable tie order);',
+             '* `tie_rows`: sampled rows with a value tie across the top-p cut (compared like any other);',
+             '* `margin_rows` / `cdf_rows`: top-p mass or `u * Z` within 1e-6 (plus the reference\'s own fp32',
+             '  normaliser error) of a boundary; `kept_differs`: margin rows whose kept count differs from the',
+             '  reference\'s; `boundary_mismatches`: tokens that differ on such rows (each still in the kept set);',
+             '* `max_prob_rel` / `max_logprob_err`: against the exact (float64) softmax / log-softmax.', '',
+             '| case | ' + ' | '.join(cols) + ' |', '|---' * (len(cols) + 1) + '|']
+    tot = dict.fromkeys(cols, 0)
+    for case, a in agg.items():
+        lines.append(f'| {case} | ' + ' | '.join(f'{a[c]:.3g}' if c.startswith('max_') else str(a[c]) for c in cols) + ' |')
+        for c in cols:
+            tot[c] = max(tot[c], a[c]) if c.startswith('max_') else tot[c] + a[c]
+    lines.append('| **all** | ' + ' | '.join(f'{tot[c]:.3g}' if c.startswith('max_') else str(tot[c]) for c in cols) + ' |')
+    print('\n'.join(lines))
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split('\n')[0])
     ap.add_argument('--gpus', type=int, default=1)
@@ -422,11 +476,14 @@ def main():
     ap.add_argument('--profile-run', action='store_true')
     ap.add_argument('--summarize-stats', metavar='DIR')
     ap.add_argument('--summarize-pmc', nargs=2, metavar=('FETCH_DIR', 'WRITE_DIR'))
+    ap.add_argument('--summarize-parity', metavar='JSONL')
     ap.add_argument('--command', nargs='*', default=[])
     args = ap.parse_args()
 
     if args.summarize_stats:
         return summarize_stats(args.summarize_stats, ' '.join(args.command))
+    if args.summarize_parity:
+        return summarize_parity(args.summarize_parity, ' '.join(args.command))
     if args.summarize_pmc:
         cmds = ' '.join(args.command).split(' ;; ')
         return summarize_pmc(*args.summarize_pmc, cmds[0], cmds[-1])
@@ -460,6 +517,9 @@ def main():
 
     res = Resident(HEADLINE, device)
     B = res.w.batch
+    from klsample import workloads
+    digests = ROOT / 'tests' / 'golden' / 'workload_digests.json'
+    digest_ok = (json.loads(digests.read_text()).get(HEADLINE) == workloads.digest(res.w)) if digests.exists() else None
     ms_step, dev_ms = timed_steps(res, args.steps, args.warmup)
     first = res.token.clone()
     scan_ms, comb_ms = phase_times(res, min(args.steps, 200))
@@ -470,12 +530,16 @@ def main():
     for name, key in (('latency_b1', 'sampled'), ('latency_b1_greedy', 'greedy')):
         r1 = Resident(name, device)
         _, d = timed_steps(r1, 1000, 100)
-        lat[key] = round(d * 1e3, 2)
+        lat[key] = round(d * 1e3, 2)                      # mean over back-to-back calls
+        groups = per_call_us(r1, 100, 10, 100)
+        lat[key + '_median'] = round(groups[len(groups) // 2], 2)   # median of 100 groups of 10 calls
+        lat[key + '_max'] = round(groups[-1], 2)
         del r1
     lat['sampler_call_wall'] = round(sampler_call_us(device), 1)
     configs = per_config(device)
 
     achieved = res.alg_bytes / (scan_ms * 1e-3) / 1e9
+    whole = res.alg_bytes / (dev_ms * 1e-3) / 1e9   # both kernels and the gaps between calls
     out = {
         'metric': METRIC,
         'value': round(B / (ms_step * 1e-3), 1),
@@ -498,9 +562,11 @@ def main():
         'kernels_us': {'scan_kernel': round(scan_ms * 1e3, 2), 'row_kernel': round(comb_ms * 1e3, 2)},
         'b1_latency_us': lat,
         'other_configs': configs,
-        'roofline': {'bound': 'hbm', 'achieved': round(achieved, 1), 'peak': PEAK_HBM_GBS, 'unit': 'GB/s',
-                     'frac': round(achieved / PEAK_HBM_GBS, 4), 'traffic': read_traffic()},
+        'roofline': {'bound': 'hbm', 'kernel': 'scan_kernel', 'achieved': round(achieved, 1), 'peak': PEAK_HBM_GBS,
+                     'unit': 'GB/s', 'frac': round(achieved / PEAK_HBM_GBS, 4), 'traffic': read_traffic(),
+                     'whole_call_achieved': round(whole, 1), 'whole_call_frac': round(whole / PEAK_HBM_GBS, 4)},
         'outputs_consistent': consistent,
+        'workload_sha256_ok': digest_ok,
     }
     if not args.no_cpu_baseline:
         out['cpu_baseline'] = cpu_baseline(args.cpu_seconds)

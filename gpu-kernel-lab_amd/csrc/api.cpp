@@ -167,6 +167,7 @@ int prepare(const klsample_batch *b, kls::Plan *plan, kls::Args *args) {
     a.params = b->params;
     a.hist_ids = b->history_ids;
     a.hist_off = b->history_offsets;
+    a.hist_errors = b->history_errors;
     a.token = b->token_ids;
     a.logprob = b->logprobs;
     a.top_ids = b->top_ids;

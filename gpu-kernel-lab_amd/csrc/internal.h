@@ -77,6 +77,7 @@ struct Args {
     const klsample_row_params *params;
     const int32_t *hist_ids;
     const int32_t *hist_off;
+    uint32_t *hist_errors;   // optional [B]: out-of-range history ids of penalised rows
     int64_t *token;
     float *logprob;
     int32_t *top_ids;

@@ -3497,6 +3497,14 @@ __device__ __forceinline__ void scan_chunk(const Args &a, int row, int chunk, un
         a.stats[(size_t)row * a.S + chunk] = st;
     }
     if (wide && !a.wide_split) wide_chunk<TIn, E>(a, row, chunk, x, mc, raw);
+    if (a.hist_errors != nullptr && chunk == 0) {
+        // (on request) the history ids outside [0, V) of a penalised row, which the
+        // counting above skipped: counted once per row, by its first chunk
+        int bad = 0;
+        for (int h = h0 + tid; h < h1; h += kThreads) bad += ((unsigned)a.hist_ids[h] >= (unsigned)V) ? 1 : 0;
+        bad = block_sum(bad, ms);
+        if (tid == 0) a.hist_errors[row] = (uint32_t)bad;
+    }
 }
 
 template <typename TIn, int E, bool kVec>

@@ -12,7 +12,7 @@ from pathlib import Path
 import numpy as np
 
 LIBRARY = Path(__file__).resolve().parent / 'libklsample.so'
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 OK = 0
 ERR_INVALID_ARGUMENT = -1
@@ -73,6 +73,7 @@ class Batch(ctypes.Structure):
         ('row_info', ctypes.c_void_p),
         ('workspace', ctypes.c_void_p),
         ('workspace_bytes', ctypes.c_size_t),
+        ('history_errors', ctypes.c_void_p),
     ]
 
 

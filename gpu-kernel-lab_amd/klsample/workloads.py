@@ -19,6 +19,7 @@ tie_stress_b1024                       1024    151936   fp32    bf16-grid ties; 
 """
 from __future__ import annotations
 
+import hashlib
 from dataclasses import dataclass
 
 import numpy as np
@@ -66,6 +67,25 @@ class Workload:
         CSR offsets (4 B)."""
         elem = self.logits.element_size()
         return self.batch * self.vocab * elem + 4 * self.history_tokens + self.batch * (32 + 8 + 4 + 4)
+
+
+def digest(w: Workload) -> str:
+    """SHA-256 of everything a workload feeds the sampler: the logits' bytes, the
+    uniforms, every history (length then ids) and every row's parameters.  The committed
+    digests detect a change of the generator (numpy's PCG64 streams, the bf16 rounding)
+    between machines."""
+    h = hashlib.sha256()
+    h.update(str((tuple(w.logits.shape), str(w.logits.dtype))).encode())
+    h.update(w.logits.contiguous().view(torch.uint8).numpy().tobytes())
+    h.update(np.ascontiguousarray(w.uniforms, dtype=np.float32).tobytes())
+    for hist in w.histories:
+        ids = np.ascontiguousarray(hist, dtype=np.int32)
+        h.update(np.int64(ids.size).tobytes())
+        h.update(ids.tobytes())
+    for p in w.params:
+        h.update(repr((p.temperature, p.top_k, p.top_p, p.repetition_penalty, sorted(p.stop_token_ids), p.seed,
+                       p.logprobs, p.presence_penalty, p.frequency_penalty)).encode())
+    return h.hexdigest()
 
 
 def _penalised(p) -> bool:

@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define KLSAMPLE_ABI_VERSION 1
+#define KLSAMPLE_ABI_VERSION 2
 
 /* status codes */
 #define KLSAMPLE_OK 0
@@ -100,6 +100,10 @@ typedef struct klsample_batch {
     klsample_row_info *row_info;            /* optional [batch] out */
     void *workspace;                        /* device scratch, see klsample_workspace_size */
     size_t workspace_bytes;
+    uint32_t *history_errors;               /* optional [batch] out: history ids of penalised rows
+                                               outside [0, vocab), which the call ignored (the
+                                               reference's scores[ids] raises on them,
+                                               serving/sampling.py:48-49); 0 for other rows */
 } klsample_batch;
 
 /* ABI version of the loaded library (KLSAMPLE_ABI_VERSION). */

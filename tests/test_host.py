@@ -1,5 +1,7 @@
 """Host-side logic of the drop-in API (CPU only)."""
 import hashlib
+import json
+from pathlib import Path
 
 import numpy as np
 import pytest
@@ -152,3 +154,14 @@ def test_workload_shapes_of_documented_configs():
     x = w1.logits.float()[0]
     assert float(x.max()) > 14  # the +8 heavy head tops the 3*N(0,1) bulk (max ~13)
     assert workloads.make('cpu_reference_b8', batch=3).batch == 3
+
+
+DIGESTS = Path(__file__).resolve().parent / 'golden' / 'workload_digests.json'
+
+
+@pytest.mark.parametrize('name', workloads.NAMES)
+def test_workloads_match_the_committed_digests(name):
+    """Every workload regenerates to the bytes whose SHA-256 is committed
+    (tests/golden/make_workload_digests.py); the GPU tests repeat this on the GPU host."""
+    want = json.loads(DIGESTS.read_text())[name]
+    assert workloads.digest(workloads.make(name)) == want

@@ -121,3 +121,62 @@ def test_integration_ctypes_stub_matches_the_drop_in():
     assert np.array_equal(tok.numpy(), want.tokens)
     assert np.array_equal(lp.numpy(), want.logprobs)
     assert np.array_equal(top_ids.numpy(), want.top_ids)
+
+
+@pytest.mark.parametrize('name', ['cpu_reference_b8', 'latency_b1', 'mixed_b64'])
+def test_workload_digests_on_the_gpu_host(name):
+    """The workloads generate the same bytes here as where the digests were committed."""
+    import json
+    from pathlib import Path
+    from klsample import workloads
+    want = json.loads((Path(__file__).resolve().parent / 'golden' / 'workload_digests.json').read_text())[name]
+    assert workloads.digest(workloads.make(name)) == want
+
+
+def test_out_of_range_history_ids_are_reported_through_the_c_abi():
+    """Ids outside [0, V) that reach the C ABI are ignored and counted per penalised row in
+    history_errors; the tokens equal those of the same call without them."""
+    import ctypes
+    from klsample import _lib
+    from klsample.runner import pack_rows
+
+    lib = _lib.load()
+    dev = torch.device('cuda', 0)
+    V = 5000
+    rng = np.random.default_rng(3)
+    logits = torch.from_numpy((rng.standard_normal((3, V)) * 2).astype(np.float32)).to(dev)
+    params = [SamplingParams(repetition_penalty=1.5), SamplingParams(temperature=0.8, top_k=20),
+              SamplingParams(temperature=0.9, repetition_penalty=1.3, frequency_penalty=0.4)]
+    good = [[1, 2, 7, 7], [4], [10, 11]]
+    bad = [[1, -5, 2, V, 7, 7, V + 100], [9999], [10, 11]]   # row 1 is not penalised
+    u = np.float32([0.0, 0.4, 0.7])
+
+    def call(hist):
+        rows, _, _, max_top_k = pack_rows(params, good, u, V)   # flags and floats only
+        ids = np.concatenate([np.asarray(h, np.int32) for h in hist])
+        offs = np.cumsum([0] + [len(h) for h in hist]).astype(np.int32)
+        d_rows = torch.from_numpy(rows.view(np.uint8).copy()).to(dev)
+        d_ids = torch.from_numpy(ids).to(dev)
+        d_off = torch.from_numpy(offs).to(dev)
+        tok = torch.empty(3, dtype=torch.int64, device=dev)
+        lp = torch.empty(3, dtype=torch.float32, device=dev)
+        errs = torch.full((3,), 77, dtype=torch.int32, device=dev)
+        ws_bytes = _lib.workspace_size(3, V, _lib.FLOAT32, max_top_k, 0)
+        ws = torch.empty(ws_bytes + 256, dtype=torch.uint8, device=dev)
+        b = _lib.Batch()
+        b.logits, b.row_stride, b.dtype, b.batch, b.vocab = logits.data_ptr(), V, _lib.FLOAT32, 3, V
+        b.max_top_k, b.params = max_top_k, d_rows.data_ptr()
+        b.history_ids, b.history_offsets = d_ids.data_ptr(), d_off.data_ptr()
+        b.token_ids, b.logprobs = tok.data_ptr(), lp.data_ptr()
+        b.workspace = ws.data_ptr() + (-ws.data_ptr()) % 256
+        b.workspace_bytes = ws_bytes
+        b.history_errors = errs.data_ptr()
+        _lib.check(lib, lib.klsample_run(ctypes.byref(b), None))
+        torch.cuda.synchronize()
+        return tok.cpu().numpy(), lp.cpu().numpy(), errs.cpu().numpy()
+
+    t_good, lp_good, e_good = call(good)
+    t_bad, lp_bad, e_bad = call(bad)
+    assert e_good.tolist() == [0, 0, 0]
+    assert e_bad.tolist() == [3, 0, 0]
+    assert np.array_equal(t_good, t_bad) and np.array_equal(lp_good, lp_bad)
