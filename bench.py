@@ -258,6 +258,39 @@ def sampler_call_us(device, calls=200):
     return (time.perf_counter() - t0) * 1e6 / calls
 
 
+def engine_step_us(device, batches=(1, 64, 256), calls=100):
+    """Host wall time of one engine-shaped step (``klsample.engine.BatchedStep``): B
+    requests with the headline row parameters, fp32 logits [B, 151936] on the GPU and
+    2048-token device histories that grow by the sampled token each step.  One step is
+    the uniform draws, the parameter and range upload, the launch, the download of the
+    results and the ``SampleResult`` objects."""
+    import torch
+    from klsample import Sampler, SamplingParams
+    from klsample.engine import BatchedStep, DeviceHistory
+    V, H = 151936, 2048
+    g = torch.Generator(device=device).manual_seed(0)
+    out = {}
+    for B in batches:
+        hist = DeviceHistory(device, V, capacity=B * (H + calls + 64), reserve=calls + 32)
+        for b in range(B):
+            hist.register(b, torch.randint(0, V, (H,), generator=g, device=device).cpu().numpy())
+        samplers = [Sampler(SamplingParams(temperature=1.0, top_k=40, top_p=0.9, repetition_penalty=1.1,
+                                           presence_penalty=0.5, frequency_penalty=0.3, seed=b), device=device)
+                    for b in range(B)]
+        logits = torch.randn(B, V, generator=g, device=device)
+        step = BatchedStep(device, hist)
+        rids = list(range(B))
+        for _ in range(10):
+            step.sample(rids, samplers, logits)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(calls):
+            step.sample(rids, samplers, logits)
+        out[f'b{B}'] = round((time.perf_counter() - t0) * 1e6 / calls, 1)
+        del hist, step, logits
+    return out
+
+
 # the other configurations of the sampling path, each timed at its own shape (device time
 # per call, inputs resident): workload name, timed calls, warm-up calls
 OTHER_CONFIGS = (
@@ -536,6 +569,7 @@ def main():
         lat[key + '_max'] = round(groups[-1], 2)
         del r1
     lat['sampler_call_wall'] = round(sampler_call_us(device), 1)
+    engine_wall = engine_step_us(device)
     configs = per_config(device)
 
     achieved = res.alg_bytes / (scan_ms * 1e-3) / 1e9
@@ -561,6 +595,7 @@ def main():
         'device_us_per_step': round(dev_ms * 1e3, 2),
         'kernels_us': {'scan_kernel': round(scan_ms * 1e3, 2), 'row_kernel': round(comb_ms * 1e3, 2)},
         'b1_latency_us': lat,
+        'engine_step_wall_us': engine_wall,
         'other_configs': configs,
         'roofline': {'bound': 'hbm', 'kernel': 'scan_kernel', 'achieved': round(achieved, 1), 'peak': PEAK_HBM_GBS,
                      'unit': 'GB/s', 'frac': round(achieved / PEAK_HBM_GBS, 4), 'traffic': read_traffic(),

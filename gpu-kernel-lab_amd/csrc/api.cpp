@@ -151,8 +151,16 @@ int prepare(const klsample_batch *b, kls::Plan *plan, kls::Args *args) {
         return fail(KLSAMPLE_ERR_INVALID_ARGUMENT, "top_ids and top_logprobs are required when num_logprobs > 0");
     if (b->history_offsets != nullptr && b->history_ids == nullptr)
         return fail(KLSAMPLE_ERR_INVALID_ARGUMENT, "history_ids must not be NULL when history_offsets is given");
-    if ((b->options & ~(uint32_t)KLSAMPLE_OPT_FORCE_DENSE) != 0)
+    if ((b->options & ~(uint32_t)(KLSAMPLE_OPT_FORCE_DENSE | KLSAMPLE_OPT_HISTORY_PAIRS | KLSAMPLE_OPT_HOST_PARAMS)) != 0)
         return fail(KLSAMPLE_ERR_INVALID_ARGUMENT, "unknown option bits 0x%x", b->options);
+    const bool host_params = (b->options & KLSAMPLE_OPT_HOST_PARAMS) != 0;
+    if (host_params && b->batch > KLSAMPLE_HOST_PARAMS_MAX_BATCH)
+        return fail(KLSAMPLE_ERR_INVALID_ARGUMENT, "KLSAMPLE_OPT_HOST_PARAMS takes at most %d rows (batch %d)",
+                    KLSAMPLE_HOST_PARAMS_MAX_BATCH, b->batch);
+    if (b->history_append != nullptr && !(b->options & KLSAMPLE_OPT_HISTORY_PAIRS))
+        return fail(KLSAMPLE_ERR_INVALID_ARGUMENT, "history_append needs KLSAMPLE_OPT_HISTORY_PAIRS");
+    if (b->history_append != nullptr && b->history_offsets == nullptr)
+        return fail(KLSAMPLE_ERR_INVALID_ARGUMENT, "history_append needs history ranges (history_offsets)");
     if (!kls::make_plan(b->batch, b->vocab, b->dtype, b->max_top_k, b->num_logprobs, plan))
         return fail(KLSAMPLE_ERR_INVALID_ARGUMENT, "batch * chunks exceeds the grid limit");
 
@@ -167,7 +175,21 @@ int prepare(const klsample_batch *b, kls::Plan *plan, kls::Args *args) {
     a.params = b->params;
     a.hist_ids = b->history_ids;
     a.hist_off = b->history_offsets;
+    a.inline_flags = 0;
+    if (host_params) {
+        // host memory: copied into the kernel arguments now, never dereferenced on the GPU
+        memcpy(a.inl_params, b->params, sizeof(klsample_row_params) * (size_t)b->batch);
+        a.params = nullptr;
+        a.inline_flags |= kls::kInlineParams;
+        if (b->history_offsets != nullptr) {
+            const int n = (b->options & KLSAMPLE_OPT_HISTORY_PAIRS) ? 2 * b->batch : b->batch + 1;
+            memcpy(a.inl_off, b->history_offsets, sizeof(int32_t) * (size_t)n);
+            a.hist_off = nullptr;
+            a.inline_flags |= kls::kInlineOffsets;
+        }
+    }
     a.hist_errors = b->history_errors;
+    a.hist_append = b->history_append;
     a.token = b->token_ids;
     a.logprob = b->logprobs;
     a.top_ids = b->top_ids;

@@ -23,6 +23,9 @@ constexpr int kMaxChunksLds = 4096;    // chunks per row the candidate combine i
 // chunk max m_c (the last bin everything further down).  Each bin is one 64-bit word:
 // the entry count above bit kWideCountShift, below it the sum of the entries'
 // fixed-point weights exp(y - G / kWideCells) in units of 2^-kWideMassBits.
+constexpr int kInlineRows = KLSAMPLE_HOST_PARAMS_MAX_BATCH;
+constexpr int32_t kInlineParams = 1;
+constexpr int32_t kInlineOffsets = 2;
 constexpr int kWideBins = 1024;
 constexpr float kWideCells = 32.f;       // bins per unit of score (natural log)
 constexpr int kWideCountShift = 50;
@@ -78,6 +81,7 @@ struct Args {
     const int32_t *hist_ids;
     const int32_t *hist_off;
     uint32_t *hist_errors;   // optional [B]: out-of-range history ids of penalised rows
+    int32_t *hist_append;    // optional: row b's token also stored at hist_append[end_b]
     int64_t *token;
     float *logprob;
     int32_t *top_ids;
@@ -94,6 +98,11 @@ struct Args {
     int32_t vec_ok;   // 16-byte vector loads are legal for every row
     int32_t xcd_map;  // place all chunks of a row on one XCD
     int32_t wide_split;  // top-p chunks' histograms from a second workgroup each (small grids)
+    // Small batches may carry their row parameters and history offsets here, in the
+    // kernel arguments, instead of in device memory (kInlineParams / kInlineOffsets).
+    int32_t inline_flags;
+    klsample_row_params inl_params[kInlineRows];
+    int32_t inl_off[2 * kInlineRows];
 };
 
 // Caller-owned hipEvent_t handles recorded around the kernels of a call (diagnostics):

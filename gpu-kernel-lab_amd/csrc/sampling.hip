@@ -96,10 +96,33 @@ __device__ __forceinline__ float penalize(float s, uint32_t count, const klsampl
     return s;
 }
 
+// The row's history as [h0, h1) in hist_ids: CSR offsets, or begin/end pairs
+// (KLSAMPLE_OPT_HISTORY_PAIRS), in memory or (kInline) possibly in the kernel
+// arguments.  Both 0 without history.
+template <bool kInline = true>
+__device__ __forceinline__ void hist_range(const Args &a, int row, int &h0, int &h1) {
+    h0 = h1 = 0;
+    const int i = (a.options & KLSAMPLE_OPT_HISTORY_PAIRS) ? 2 * row : row;
+    if (kInline && (a.inline_flags & kInlineOffsets)) {
+        h0 = a.inl_off[i];
+        h1 = a.inl_off[i + 1];
+        return;
+    }
+    if (a.hist_off == nullptr) return;
+    h0 = a.hist_off[i];
+    h1 = a.hist_off[i + 1];
+}
+
+// The row's parameters, from memory or from the kernel arguments.
+__device__ __forceinline__ klsample_row_params row_params(const Args &a, int row) {
+    return (a.inline_flags & kInlineParams) ? a.inl_params[row] : a.params[row];
+}
+
 __device__ __forceinline__ bool has_penalty(const Args &a, const klsample_row_params &p, int row) {
     if (!(p.flags & (KLSAMPLE_ROW_REPETITION | KLSAMPLE_ROW_PRESENCE_FREQUENCY))) return false;
-    if (a.hist_off == nullptr) return false;
-    return a.hist_off[row + 1] > a.hist_off[row];
+    int h0, h1;
+    hist_range(a, row, h0, h1);
+    return h1 > h0;
 }
 
 // ---------------------------------------------------------------------------------
@@ -342,7 +365,8 @@ __device__ __forceinline__ void build_counts(uint32_t *cnt, const Args &a, int r
     uint4 *c4 = reinterpret_cast<uint4 *>(cnt);
     for (int i = threadIdx.x; i < C / 4; i += kThreads) c4[i] = make_uint4(0u, 0u, 0u, 0u);
     __syncthreads();
-    const int h0 = a.hist_off[row], h1 = a.hist_off[row + 1];
+    int h0, h1;
+    hist_range(a, row, h0, h1);
     // eight independent loads in flight per thread before any LDS atomic
     for (int hb = h0 + (int)threadIdx.x; hb < h1; hb += 8 * kThreads) {
         int id[8];
@@ -1155,6 +1179,15 @@ __device__ __forceinline__ void sort_keys(unsigned long long *sb, int n, uint32_
 // ---------------------------------------------------------------------------------
 // Outputs of a resolved row.
 
+// With hist_append (history ranges as begin/end pairs), the row's token is also stored
+// just past its history, so the caller's next range is one longer.
+__device__ __forceinline__ void append_token(const Args &a, int row, int token) {
+    if (a.hist_append == nullptr) return;
+    int h0, h1;
+    hist_range(a, row, h0, h1);
+    a.hist_append[h1] = token;
+}
+
 struct RowOut {
     int token;
     double logprob;
@@ -1209,6 +1242,7 @@ __device__ __forceinline__ void write_row(const Args &a, int row, int mode, cons
     }
     if (threadIdx.x == 0) {
         a.token[row] = r.token;
+        append_token(a, row, r.token);
         a.logprob[row] = (float)r.logprob;
         klsample_row_info info;
         info.max_score = r.m;
@@ -1448,7 +1482,9 @@ __device__ __forceinline__ void dense_resolve(const Args &a, int row, const klsa
     // chunk's 256-element rows coalesced), the next chunk's requested before the current
     // one is penalised and written.  A history of at most kMaxChunksLds ids is kept in
     // LDS and counted from there per chunk; a longer one is re-read per chunk.
-    const int h0 = pen ? a.hist_off[row] : 0, H = pen ? a.hist_off[row + 1] - h0 : 0;
+    int h0 = 0, h1 = 0;
+    if (pen) hist_range(a, row, h0, h1);
+    const int H = h1 - h0;
     const bool ids_lds = H <= kMaxChunksLds;
     if (pen && ids_lds) {
         for (int hb = 0; hb < H; hb += 8 * kThreads) {
@@ -2212,6 +2248,7 @@ __device__ __forceinline__ void wave_write(const Args &a, int row, int mode, con
     }
     if (l == 0) {
         a.token[row] = r.token;
+        append_token(a, row, r.token);
         a.logprob[row] = (float)r.logprob;
         klsample_row_info info;
         info.max_score = r.m;
@@ -3133,13 +3170,16 @@ __device__ __forceinline__ void wide_chunk(const Args &a, int row, int chunk, co
 // penalises the marked ones there (one per set mask bit) and reloads them, so the
 // dense work that follows (bound, candidates, sums) sees final scores everywhere
 // with no per-element branch.
-template <typename TIn, int E, bool kVec>
+// kInline: a launch whose row parameters (and maybe history offsets) are in the kernel
+// arguments (small batches); a separate instantiation keeps the branch out of the
+// streaming pass's register budget.
+template <typename TIn, int E, bool kVec, bool kInline>
 __device__ __forceinline__ void scan_chunk(const Args &a, int row, int chunk, unsigned char *raw, ScanMisc &ms,
                                            bool wide_only) {
     constexpr int VW = Loader<TIn>::VW;
     constexpr int NV = E / VW;
     constexpr int C = kThreads * E;
-    const klsample_row_params p = a.params[row];
+    const klsample_row_params p = kInline ? a.inl_params[row] : a.params[row];
     const int V = a.V;
     const int tid = threadIdx.x;
     const int mode = row_mode(p, V);
@@ -3157,11 +3197,8 @@ __device__ __forceinline__ void scan_chunk(const Args &a, int row, int chunk, un
     // path below.
     // (the offsets are requested with the parameters, not after them: one memory round
     // trip before the loads start)
-    int h0 = 0, h1 = 0;
-    if (a.hist_off != nullptr) {
-        h0 = a.hist_off[row];
-        h1 = a.hist_off[row + 1];
-    }
+    int h0, h1;
+    hist_range<kInline>(a, row, h0, h1);
     if (!(p.flags & (KLSAMPLE_ROW_REPETITION | KLSAMPLE_ROW_PRESENCE_FREQUENCY))) h1 = h0;
     const int H = h1 - h0;
     // 16-bit counts (two per word) cover the chunk when no count can reach 65536;
@@ -3507,15 +3544,17 @@ __device__ __forceinline__ void scan_chunk(const Args &a, int row, int chunk, un
     }
 }
 
-template <typename TIn, int E, bool kVec>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(E >= 32 ? 6 : E >= 16 ? 7 : 8))) void scan_kernel(Args a) {
+// (a launch with inline parameters has at most KLSAMPLE_HOST_PARAMS_MAX_BATCH rows, a few
+// workgroups per CU at most: its register budget is not traded for occupancy)
+template <typename TIn, int E, bool kVec, bool kInline>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(kInline ? 4 : E >= 32 ? 6 : E >= 16 ? 7 : 8))) void scan_kernel(Args a) {
     __shared__ __attribute__((aligned(16))) unsigned char raw[ScanLds<E>::value];
     __shared__ ScanMisc ms;
     // blocks past B * S are the second workgroups of top-p chunks (a.wide_split)
     const bool wide_only = blockIdx.x >= (unsigned)(a.B * a.S);
     int row, chunk;
     map_block(a, wide_only ? (int)blockIdx.x - a.B * a.S : (int)blockIdx.x, row, chunk);
-    scan_chunk<TIn, E, kVec>(a, row, chunk, raw, ms, wide_only);
+    scan_chunk<TIn, E, kVec, kInline>(a, row, chunk, raw, ms, wide_only);
 }
 
 template <int C>
@@ -3593,7 +3632,8 @@ __device__ __forceinline__ void row_body(const Args &a, int row, unsigned char *
     // the vector memory path, so that waiting for them waits for nothing else)
     RowSpec rs;
     request_row(a, row, rs);
-    const klsample_row_params p = load_params_vmem(a.params, row);
+    const klsample_row_params p =
+        (a.inline_flags & kInlineParams) ? a.inl_params[row] : load_params_vmem(a.params, row);
     const int mode = row_mode(p, a.V);
     const bool force = (a.options & KLSAMPLE_OPT_FORCE_DENSE) != 0;
     bool done = false;
@@ -3626,7 +3666,7 @@ __global__ __launch_bounds__(kThreads) void probs_kernel(Args a) {
     __shared__ __attribute__((aligned(16))) uint32_t cnt[C];
     int row, chunk;
     map_block(a, blockIdx.x, row, chunk);
-    const klsample_row_params p = a.params[row];
+    const klsample_row_params p = row_params(a, row);
     const int mode = row_mode(p, a.V);
     const klsample_row_info ri = a.rows[row];
     const int c0 = chunk * C, cn = min(C, a.V - c0);
@@ -3664,8 +3704,13 @@ hipError_t launch_typed(const Args &a, hipStream_t s, const PhaseEvents *ph) {
     // 16-byte loads need aligned rows and a last chunk of at least one vector
     const int tail = a.V - (a.S - 1) * a.C;
     const bool vec = a.vec_ok && tail * (int)sizeof(TIn) >= 16;
-    if (vec) scan_kernel<TIn, E, true><<<scan_grid, kThreads, 0, s>>>(a);
-    else scan_kernel<TIn, E, false><<<scan_grid, kThreads, 0, s>>>(a);
+    if (a.inline_flags & kInlineParams) {
+        if (vec) scan_kernel<TIn, E, true, true><<<scan_grid, kThreads, 0, s>>>(a);
+        else scan_kernel<TIn, E, false, true><<<scan_grid, kThreads, 0, s>>>(a);
+    } else {
+        if (vec) scan_kernel<TIn, E, true, false><<<scan_grid, kThreads, 0, s>>>(a);
+        else scan_kernel<TIn, E, false, false><<<scan_grid, kThreads, 0, s>>>(a);
+    }
     if ((e = mark(ph, 1, s)) != hipSuccess) return e;
     row_kernel<TIn, E><<<dim3((unsigned)a.B), kThreads, 0, s>>>(a);
     if ((e = mark(ph, 2, s)) != hipSuccess) return e;

@@ -12,7 +12,7 @@ from pathlib import Path
 import numpy as np
 
 LIBRARY = Path(__file__).resolve().parent / 'libklsample.so'
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 OK = 0
 ERR_INVALID_ARGUMENT = -1
@@ -29,6 +29,9 @@ ROW_PRESENCE_FREQUENCY = 4
 ROW_TOP_P = 8
 
 OPT_FORCE_DENSE = 1
+OPT_HISTORY_PAIRS = 2
+OPT_HOST_PARAMS = 4
+HOST_PARAMS_MAX_BATCH = 8
 
 MAX_LOGPROBS = 256
 MAX_BATCH = 65536
@@ -74,6 +77,7 @@ class Batch(ctypes.Structure):
         ('workspace', ctypes.c_void_p),
         ('workspace_bytes', ctypes.c_size_t),
         ('history_errors', ctypes.c_void_p),
+        ('history_append', ctypes.c_void_p),
     ]
 
 
@@ -120,6 +124,23 @@ def load(path: Path | str | None = None) -> ctypes.CDLL:
         if path is None:
             _lib = lib
         return lib
+
+
+_hip = None
+
+
+def mapped_pointer(host_ptr: int) -> int | None:
+    """The device's address of pinned host memory (``hipHostGetDevicePointer``), or
+    None if the runtime does not map it for the device."""
+    global _hip
+    if _hip is None:
+        _hip = ctypes.CDLL('libamdhip64.so')
+        _hip.hipHostGetDevicePointer.restype = ctypes.c_int
+        _hip.hipHostGetDevicePointer.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_void_p, ctypes.c_uint]
+    dev = ctypes.c_void_p()
+    if _hip.hipHostGetDevicePointer(ctypes.byref(dev), ctypes.c_void_p(host_ptr), 0) != 0 or not dev.value:
+        return None
+    return dev.value
 
 
 def last_error(lib: ctypes.CDLL) -> str:

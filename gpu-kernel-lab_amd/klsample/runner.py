@@ -1,9 +1,13 @@
 """Device-side execution of batched sampling calls through the C ABI.
 
 A :class:`DeviceRunner` owns, per GPU and per host thread, the library workspace and
-the staging buffers of a call: one pinned host buffer carrying the row parameters and
-the CSR history up in a single copy, and one device output arena brought back in a
-single copy.  Buffers only grow; a call allocates nothing once they are large enough.
+the staging buffers of a call.  Batches of up to ``HOST_PARAMS_MAX_BATCH`` rows hand
+their row parameters and history offsets to the library in host memory, which carries
+them in the kernel arguments; larger batches stage them, with any history ids, in one
+pinned buffer brought up in a single copy.  The kernels write the outputs into a pinned
+host buffer mapped for the device (or a device buffer brought back in one copy where
+the device cannot address it).  Buffers only grow; a call allocates nothing once they
+are large enough.
 """
 from __future__ import annotations
 
@@ -41,40 +45,48 @@ def normalize_history(history, vocab: int) -> np.ndarray:
     return ids.astype(np.int32, copy=False)
 
 
-def pack_rows(params_list, histories, uniforms, vocab: int):
-    """Row parameters (``klsample_row_params``), CSR history and ``max_top_k``.
+def row_flags(p) -> int:
+    """``KLSAMPLE_ROW_*`` flags of one request: the reference's tests on the original
+    Python values (``serving/sampling.py:47``, ``:50``, ``:56``)."""
+    flags = 0
+    if p.temperature == 0:
+        flags |= _lib.ROW_GREEDY
+    if p.repetition_penalty != 1:
+        flags |= _lib.ROW_REPETITION
+    if getattr(p, 'presence_penalty', 0.0) != 0 or getattr(p, 'frequency_penalty', 0.0) != 0:
+        flags |= _lib.ROW_PRESENCE_FREQUENCY
+    if p.top_p < 1:
+        flags |= _lib.ROW_TOP_P
+    return flags
 
-    The flags carry the reference's tests on the original Python values
-    (``serving/sampling.py:47``, ``:50``, ``:56``); the floats are their fp32 roundings,
-    which is what the reference's tensor-by-scalar operations use.
-    """
+
+def row_record(p, uniform: float = 0.0) -> np.ndarray:
+    """One ``klsample_row_params`` record (an array of one).  The floats are the fp32
+    roundings of the Python values, which is what the reference's tensor-by-scalar
+    operations use."""
+    rec = np.zeros(1, dtype=_lib.ROW_PARAMS_DTYPE)
+    rec[0] = (p.temperature, min(int(p.top_k), _INT32_MAX), p.top_p, p.repetition_penalty,
+              getattr(p, 'presence_penalty', 0.0), getattr(p, 'frequency_penalty', 0.0),
+              0.0 if p.temperature == 0 else uniform, row_flags(p))
+    return rec
+
+
+def max_top_k_of(params_list, vocab: int) -> int:
+    """Largest top-k of the sampled rows (sizes the candidate slots), 0 if none."""
+    return max([min(int(p.top_k), vocab) for p in params_list if p.temperature != 0 and p.top_k > 0] or [0])
+
+
+def pack_rows(params_list, histories, uniforms, vocab: int):
+    """Row parameters (``klsample_row_params``), CSR history and ``max_top_k``."""
     B = len(params_list)
     rows = np.zeros(B, dtype=_lib.ROW_PARAMS_DTYPE)
     offsets = np.zeros(B + 1, dtype=np.int32)
     chunks = []
     total = 0
-    max_top_k = 0
     for b, p in enumerate(params_list):
-        flags = 0
-        greedy = p.temperature == 0
-        if greedy:
-            flags |= _lib.ROW_GREEDY
-        rep = p.repetition_penalty != 1
-        pf = getattr(p, 'presence_penalty', 0.0) != 0 or getattr(p, 'frequency_penalty', 0.0) != 0
-        if rep:
-            flags |= _lib.ROW_REPETITION
-        if pf:
-            flags |= _lib.ROW_PRESENCE_FREQUENCY
-        if p.top_p < 1:
-            flags |= _lib.ROW_TOP_P
-        top_k = min(int(p.top_k), _INT32_MAX)
-        rows[b] = (p.temperature, top_k, p.top_p, p.repetition_penalty,
-                   getattr(p, 'presence_penalty', 0.0), getattr(p, 'frequency_penalty', 0.0),
-                   0.0 if uniforms is None or greedy else uniforms[b], flags)
-        if not greedy and top_k > 0:
-            max_top_k = max(max_top_k, min(top_k, vocab))
+        rows[b] = row_record(p, 0.0 if uniforms is None else uniforms[b])[0]
         hist = histories[b] if histories is not None else ()
-        if (rep or pf) and len(hist):
+        if (int(rows['flags'][b]) & (_lib.ROW_REPETITION | _lib.ROW_PRESENCE_FREQUENCY)) and len(hist):
             ids = normalize_history(hist, vocab)
             chunks.append(ids)
             total += ids.size
@@ -82,7 +94,7 @@ def pack_rows(params_list, histories, uniforms, vocab: int):
     if total > _INT32_MAX:
         raise ValueError('total history length exceeds the int32 CSR offsets')
     ids = np.concatenate(chunks) if chunks else np.zeros(0, dtype=np.int32)
-    return rows, offsets, ids, max_top_k
+    return rows, offsets, ids, max_top_k_of(params_list, vocab)
 
 
 @dataclass
@@ -139,20 +151,23 @@ class DeviceRunner:
         self.stage_host = torch.empty(n, dtype=torch.uint8, pin_memory=True)
 
     def _ensure_out(self, nbytes: int) -> None:
-        if self.out_dev is not None and self.out_dev.numel() >= nbytes:
+        if self.out_host is not None and self.out_host.numel() >= nbytes:
             return
         n = _align(max(nbytes, 4096), 4096)
-        self.out_dev = torch.empty(n, dtype=torch.uint8, device=self.device)
         self.out_host = torch.empty(n, dtype=torch.uint8, pin_memory=True)
+        # the kernels write the outputs straight into this pinned buffer when the device
+        # can address it; otherwise into a device twin copied back after the launch
+        mapped = _lib.mapped_pointer(self.out_host.data_ptr())
+        self.out_dev = None if mapped is not None else torch.empty(n, dtype=torch.uint8, device=self.device)
+        self.out_ptr = mapped if mapped is not None else self.out_dev.data_ptr()
 
     # -- one call ------------------------------------------------------------------------
+    @torch.inference_mode()   # the buffers may have been made as inference tensors by an earlier call
     def run(self, logits: torch.Tensor, params_list, histories, uniforms, num_logprobs: int, *,
             options: int = 0, want_probs: bool = False, want_info: bool = False) -> BatchOutput:
         """Sample every row of ``logits`` ([B, V] on this device) and wait for the result."""
         if logits.dim() != 2:
             raise ValueError('logits must be [batch, vocab]')
-        if logits.dtype not in _DTYPES:
-            logits = logits.float()
         B, V = logits.shape
         # the kernels read one parameter record, CSR offset pair and uniform per logits row
         if len(params_list) != B:
@@ -161,56 +176,89 @@ class DeviceRunner:
             raise ValueError(f'one history per row is required ({len(histories)} for {B} rows)')
         if uniforms is not None and len(uniforms) != B:
             raise ValueError(f'one uniform per row is required ({len(uniforms)} for {B} rows)')
+        rows, offsets, ids, max_top_k = pack_rows(params_list, histories, uniforms, V)
+        out = self.run_packed(logits, rows, max_top_k, int(num_logprobs),
+                              offsets=offsets if ids.size else None, ids=ids if ids.size else None,
+                              options=options, want_probs=want_probs, want_info=want_info)
+        tokens, logprobs, top_ids, top_lp, info, probs = out
+        return BatchOutput(tokens.copy(), logprobs.copy(), top_ids.copy(), top_lp.copy(),
+                           info.copy() if info is not None else None, probs, V)
+
+    @torch.inference_mode()
+    def run_packed(self, logits: torch.Tensor, rows: np.ndarray, max_top_k: int, N: int, *,
+                   offsets: np.ndarray | None = None, ids: np.ndarray | None = None, ids_ptr: int | None = None,
+                   append_ptr: int | None = None, options: int = 0, want_probs: bool = False,
+                   want_info: bool = False):
+        """One library call on packed rows (``klsample_row_params`` records) and wait.
+
+        ``offsets`` are the history offsets (CSR, or begin/end pairs with
+        ``OPT_HISTORY_PAIRS``) into ``ids`` (host, uploaded with the call) or into device
+        ids at ``ids_ptr``; ``append_ptr`` is ``history_append``.  Up to
+        ``HOST_PARAMS_MAX_BATCH`` rows travel in the kernel arguments (nothing is
+        uploaded without host ids).  Returns host views of tokens, logprobs, top ids, top
+        logprobs and row info (valid until the next call on this runner) and the device
+        probabilities."""
+        if logits.dtype not in _DTYPES:
+            logits = logits.float()
+        B, V = logits.shape
         # rows must not overlap (a size-1 dimension may carry any stride)
         if logits.stride(1) != 1 or (B > 1 and logits.stride(0) < V):
             logits = logits.contiguous()
-        row_stride = logits.stride(0) if B > 1 else V
-        N = int(num_logprobs)
-        rows, offsets, ids, max_top_k = pack_rows(params_list, histories, uniforms, V)
         stream = torch.cuda.current_stream(self.device)
         sptr = stream.cuda_stream
+        dt = _DTYPES[logits.dtype]
+        self._ensure_workspace(_lib.workspace_size(B, V, dt, max_top_k, N), sptr)
+        batch = _lib.Batch()
+        host_params = B <= _lib.HOST_PARAMS_MAX_BATCH
+        # one host-to-device copy, if any: params | offsets (larger batches) | ids
+        o_off = _align(rows.nbytes) if not host_params else 0
+        o_ids = _align(o_off + offsets.nbytes) if offsets is not None and not host_params else o_off
+        stage_bytes = _align(o_ids + (ids.nbytes if ids is not None else 0))
+        if stage_bytes:
+            self._ensure_stage(stage_bytes)
+            host = self.stage_host.numpy()
+            if not host_params:
+                host[:rows.nbytes] = rows.view(np.uint8)
+                if offsets is not None:
+                    host[o_off:o_off + offsets.nbytes] = offsets.view(np.uint8)
+            if ids is not None:
+                host[o_ids:o_ids + ids.nbytes] = ids.view(np.uint8)
+            self.stage_dev[:stage_bytes].copy_(self.stage_host[:stage_bytes], non_blocking=True)
+            dbase = self.stage_dev.data_ptr()
+        if host_params:
+            options |= _lib.OPT_HOST_PARAMS
+            batch.params = rows.ctypes.data
+            if offsets is not None:
+                batch.history_offsets = offsets.ctypes.data
+        else:
+            batch.params = dbase
+            if offsets is not None:
+                batch.history_offsets = dbase + o_off
+        if ids is not None:
+            batch.history_ids = dbase + o_ids
+        elif ids_ptr is not None:
+            batch.history_ids = ids_ptr
+        batch.history_append = append_ptr
 
-        ws_bytes = _lib.workspace_size(B, V, _DTYPES[logits.dtype], max_top_k, N)
-        self._ensure_workspace(ws_bytes, sptr)
-
-        # one host-to-device copy: params | offsets | ids
-        o_par = 0
-        o_off = _align(o_par + rows.nbytes)
-        o_ids = _align(o_off + offsets.nbytes)
-        stage_bytes = _align(o_ids + ids.nbytes)
-        self._ensure_stage(stage_bytes)
-        host = self.stage_host.numpy()
-        host[o_par:o_par + rows.nbytes] = rows.view(np.uint8)
-        host[o_off:o_off + offsets.nbytes] = offsets.view(np.uint8)
-        if ids.size:
-            host[o_ids:o_ids + ids.nbytes] = ids.view(np.uint8)
-        self.stage_dev[:stage_bytes].copy_(self.stage_host[:stage_bytes], non_blocking=True)
-        dbase = self.stage_dev.data_ptr()
-
-        # one device-to-host copy: tokens | logprobs | top ids | top logprobs | info
-        p_tok = 0
-        p_lp = _align(p_tok + 8 * B)
+        # outputs: tokens | logprobs | top ids | top logprobs | info
+        p_lp = _align(8 * B)
         p_tid = _align(p_lp + 4 * B)
         p_tlp = _align(p_tid + 4 * B * N)
         p_inf = _align(p_tlp + 4 * B * N)
         out_bytes = _align(p_inf + (_lib.ROW_INFO_DTYPE.itemsize * B if want_info else 0))
         self._ensure_out(out_bytes)
-        obase = self.out_dev.data_ptr()
+        obase = self.out_ptr
         probs = torch.empty((B, V), dtype=torch.float32, device=self.device) if want_probs else None
 
-        batch = _lib.Batch()
         batch.logits = logits.data_ptr()
-        batch.row_stride = row_stride
-        batch.dtype = _DTYPES[logits.dtype]
+        batch.row_stride = logits.stride(0) if B > 1 else V
+        batch.dtype = dt
         batch.batch = B
         batch.vocab = V
         batch.num_logprobs = N
         batch.max_top_k = max_top_k
         batch.options = options
-        batch.params = dbase + o_par
-        batch.history_ids = dbase + o_ids if ids.size else None
-        batch.history_offsets = dbase + o_off if ids.size else None
-        batch.token_ids = obase + p_tok
+        batch.token_ids = obase
         batch.logprobs = obase + p_lp
         batch.top_ids = obase + p_tid if N else None
         batch.top_logprobs = obase + p_tlp if N else None
@@ -219,16 +267,16 @@ class DeviceRunner:
         batch.workspace = self.workspace_ptr
         batch.workspace_bytes = self.workspace_bytes
         _lib.check(self.lib, self.lib.klsample_run(ctypes.byref(batch), ctypes.c_void_p(sptr)))
-
-        self.out_host[:out_bytes].copy_(self.out_dev[:out_bytes], non_blocking=True)
+        if self.out_dev is not None:
+            self.out_host[:out_bytes].copy_(self.out_dev[:out_bytes], non_blocking=True)
         stream.synchronize()
         h = self.out_host.numpy()
-        tokens = h[p_tok:p_tok + 8 * B].view(np.int64).copy()
-        logprobs = h[p_lp:p_lp + 4 * B].view(np.float32).copy()
-        top_ids = h[p_tid:p_tid + 4 * B * N].view(np.int32).reshape(B, N).copy()
-        top_lp = h[p_tlp:p_tlp + 4 * B * N].view(np.float32).reshape(B, N).copy()
-        info = h[p_inf:p_inf + _lib.ROW_INFO_DTYPE.itemsize * B].view(_lib.ROW_INFO_DTYPE).copy() if want_info else None
-        return BatchOutput(tokens, logprobs, top_ids, top_lp, info, probs, V)
+        tokens = h[:8 * B].view(np.int64)
+        logprobs = h[p_lp:p_lp + 4 * B].view(np.float32)
+        top_ids = h[p_tid:p_tid + 4 * B * N].view(np.int32).reshape(B, N)
+        top_lp = h[p_tlp:p_tlp + 4 * B * N].view(np.float32).reshape(B, N)
+        info = h[p_inf:p_inf + _lib.ROW_INFO_DTYPE.itemsize * B].view(_lib.ROW_INFO_DTYPE) if want_info else None
+        return tokens, logprobs, top_ids, top_lp, info, probs
 
 
 _local = threading.local()

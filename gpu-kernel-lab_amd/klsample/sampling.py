@@ -23,7 +23,9 @@ from dataclasses import dataclass
 import torch
 
 from . import _lib
-from .runner import runner_for, target_device
+from .runner import row_record, runner_for, target_device
+
+_UNIFORM_BLOCK = 64
 
 
 @dataclass(frozen=True)
@@ -73,6 +75,8 @@ class Sampler:
     def __init__(self, params: SamplingParams, device='cpu'):
         self.params = params
         self.generators = {}
+        self.uniforms = {}    # device key -> [block of uniforms, next index]
+        self.record = None    # the packed klsample_row_params of params
         if device is not None:
             self._generator(torch.device(device))
 
@@ -85,15 +89,43 @@ class Sampler:
         return self.generators[key]
 
     def next_uniform(self, device) -> float:
-        """The uniform of this request's next sampled call."""
-        return float(torch.rand((), generator=self._generator(device)))
+        """The uniform of this request's next sampled call.
+
+        Uniforms are drawn from the generator in blocks of 64 and served in order: a
+        block draw yields the same sequence as 64 single draws, at the cost of about one.
+        The generator's own state therefore runs up to 63 draws ahead of the calls."""
+        key = str(device)
+        block = self.uniforms.get(key)
+        if block is None or block[1] == len(block[0]):
+            block = self.uniforms[key] = [torch.rand(_UNIFORM_BLOCK, generator=self._generator(device)).tolist(), 0]
+        u = block[0][block[1]]
+        block[1] += 1
+        return u
 
     @torch.inference_mode()
     def sample(self, logits: torch.Tensor, history=()) -> SampleResult:
         if logits.ndim != 1 or not logits.is_floating_point():
             raise ValueError('logits must be a floating vector')
-        u = self.next_uniform(logits.device) if self.params.temperature != 0 else 0.0
-        return _run([logits], [self.params], [history], [u])[0]
+        p = self.params
+        u = self.next_uniform(logits.device) if p.temperature != 0 else 0.0
+        if self.record is None:
+            self.record = row_record(p)
+        rec = self.record
+        if (int(rec['flags'][0]) & (_lib.ROW_REPETITION | _lib.ROW_PRESENCE_FREQUENCY)) and len(history):
+            return _run([logits], [p], [history], [u])[0]
+        # no history to apply: the packed record goes to the library as it is
+        device = target_device(logits)
+        if logits.device != device:
+            logits = logits.to(device)
+        V = logits.numel()
+        rec['uniform'][0] = u
+        N = min(p.logprobs, _lib.MAX_LOGPROBS)
+        top_k = min(int(p.top_k), V) if p.temperature != 0 and p.top_k > 0 else 0
+        tokens, lps, tids, tlps, _, _ = runner_for(device).run_packed(logits.unsqueeze(0), rec, top_k, N)
+        token = int(tokens[0])
+        n = min(p.logprobs, V, N)
+        return SampleResult(token, float(lps[0]), tuple(zip(tids[0, :n].tolist(), tlps[0, :n].tolist())),
+                            token in p.stop_token_ids)
 
     @staticmethod
     @torch.inference_mode()

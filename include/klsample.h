@@ -27,7 +27,7 @@
 extern "C" {
 #endif
 
-#define KLSAMPLE_ABI_VERSION 2
+#define KLSAMPLE_ABI_VERSION 3
 
 /* status codes */
 #define KLSAMPLE_OK 0
@@ -49,6 +49,12 @@ extern "C" {
 
 /* klsample_batch.options */
 #define KLSAMPLE_OPT_FORCE_DENSE 1u       /* resolve every row on the multi-pass path (testing) */
+#define KLSAMPLE_OPT_HISTORY_PAIRS 2u     /* history_offsets holds [begin, end) per row (2 * batch
+                                             entries) into a shared id arena, instead of CSR */
+#define KLSAMPLE_OPT_HOST_PARAMS 4u       /* params and history_offsets are HOST memory, read before
+                                             the call returns and carried in the kernel arguments
+                                             (no upload): batch <= KLSAMPLE_HOST_PARAMS_MAX_BATCH */
+#define KLSAMPLE_HOST_PARAMS_MAX_BATCH 8
 
 /* Per-row sampling parameters (32 bytes).  Mirrors SamplingParams
  * (serving/sampling.py:8-15) plus presence/frequency and the row's uniform.
@@ -91,7 +97,8 @@ typedef struct klsample_batch {
     uint32_t options;           /* KLSAMPLE_OPT_* */
     const klsample_row_params *params;      /* [batch] */
     const int32_t *history_ids;             /* CSR token history; ids in [0, vocab) */
-    const int32_t *history_offsets;         /* [batch + 1]; NULL means no history */
+    const int32_t *history_offsets;         /* [batch + 1] (CSR), or [2 * batch] begin/end pairs with
+                                               KLSAMPLE_OPT_HISTORY_PAIRS; NULL means no history */
     int64_t *token_ids;                     /* [batch] out */
     float *logprobs;                        /* [batch] out: log-softmax of the sampled token */
     int32_t *top_ids;                       /* [batch * num_logprobs] out, or NULL if N == 0 */
@@ -104,6 +111,12 @@ typedef struct klsample_batch {
                                                outside [0, vocab), which the call ignored (the
                                                reference's scores[ids] raises on them,
                                                serving/sampling.py:48-49); 0 for other rows */
+    int32_t *history_append;                /* optional, with KLSAMPLE_OPT_HISTORY_PAIRS: row b's
+                                               token is also stored at history_append[end_b] (the
+                                               arena as writable memory, room reserved by the
+                                               caller), so the next call's range is [begin_b,
+                                               end_b + 1): the engine's prompt + generated
+                                               (serving/engine.py:94) without re-uploading it */
 } klsample_batch;
 
 /* ABI version of the loaded library (KLSAMPLE_ABI_VERSION). */

@@ -159,6 +159,47 @@ int main() {
         CHECK(klsample_run_noalloc(&kb, nullptr) == KLSAMPLE_ERR_WORKSPACE);
     }
 
+    // host parameters: copied into the launch arguments (exact sizes, so that an overread
+    // is caught), history offsets too; more than the inline rows is an argument error
+    for (int B = 1; B <= KLSAMPLE_HOST_PARAMS_MAX_BATCH; B += 7) {
+        for (int pairs = 0; pairs < 2; ++pairs) {
+            Bufs b;
+            klsample_batch k = make_batch(b, B, 5000, 2, 40);
+            std::vector<klsample_row_params> hp(B);
+            for (int i = 0; i < B; ++i) hp[i].top_k = 7 + i;
+            std::vector<int32_t> ho(pairs ? 2 * B : B + 1);
+            for (size_t i = 0; i < ho.size(); ++i) ho[i] = (int32_t)(3 * i);
+            k.params = hp.data();
+            k.history_offsets = ho.data();
+            k.options = KLSAMPLE_OPT_HOST_PARAMS | (pairs ? KLSAMPLE_OPT_HISTORY_PAIRS : 0u);
+            if (pairs) k.history_append = b.ids.data();
+            CHECK(klsample_run(&k, nullptr) == KLSAMPLE_OK);
+            const kls::Args &a = stub::last_args;
+            CHECK(a.params == nullptr && a.hist_off == nullptr);
+            CHECK(a.inline_flags == (kls::kInlineParams | kls::kInlineOffsets));
+            CHECK(a.inl_params[B - 1].top_k == 7 + B - 1 && a.inl_off[ho.size() - 1] == ho.back());
+            CHECK(a.hist_append == (pairs ? b.ids.data() : nullptr));
+            k.history_offsets = nullptr;
+            k.history_append = nullptr;
+            CHECK(klsample_run(&k, nullptr) == KLSAMPLE_OK);
+            CHECK(stub::last_args.inline_flags == kls::kInlineParams);
+        }
+    }
+    {
+        Bufs b;
+        klsample_batch k = make_batch(b, KLSAMPLE_HOST_PARAMS_MAX_BATCH + 1, 5000, 0, 0);
+        k.options = KLSAMPLE_OPT_HOST_PARAMS;
+        expect_error(&k, KLSAMPLE_ERR_INVALID_ARGUMENT);
+        k.options = 0;
+        CHECK(klsample_run(&k, nullptr) == KLSAMPLE_OK && stub::last_args.inline_flags == 0);
+        // history_append needs history pairs and their ranges
+        k.history_append = b.ids.data();
+        expect_error(&k, KLSAMPLE_ERR_INVALID_ARGUMENT);
+        k.options = KLSAMPLE_OPT_HISTORY_PAIRS;
+        k.history_offsets = nullptr;
+        expect_error(&k, KLSAMPLE_ERR_INVALID_ARGUMENT);
+    }
+
     // workspace init and phase events
     {
         unsigned char buf[64];

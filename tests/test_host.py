@@ -126,6 +126,18 @@ def test_uniform_stream_is_per_request_and_seeded():
     assert c.next_uniform('cpu') != ua[0]
 
 
+def test_uniforms_served_from_blocks_equal_single_draws():
+    """Sampler.next_uniform draws 64 at a time; the values it hands out, across block
+    boundaries, are the ones single draws of a generator with the request's seed give."""
+    s = Sampler(SamplingParams(temperature=1.0, seed=77))
+    g = torch.Generator().manual_seed(77)
+    got = [s.next_uniform('cpu') for _ in range(150)]
+    want = [float(torch.rand((), generator=g)) for _ in range(150)]
+    assert got == want
+    # a second device key has a stream of its own, from the same seed
+    assert s.next_uniform('cuda:0') == want[0]
+
+
 def _digest(t: torch.Tensor) -> str:
     return hashlib.sha256(t.contiguous().view(torch.uint8).numpy().tobytes()).hexdigest()[:16]
 

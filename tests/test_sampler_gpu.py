@@ -54,6 +54,15 @@ def test_batching_does_not_change_a_requests_tokens():
         assert one == many
 
 
+def test_entry_points_mix_inside_and_outside_inference_mode():
+    """Sampler.sample runs under inference mode and makes the staging buffers there;
+    sample_batch called afterwards outside inference mode reuses them."""
+    x = torch.randn(2, 1000).cuda()
+    a = Sampler(SamplingParams()).sample(x[0])
+    res = sample_batch(x, [SamplingParams(), SamplingParams()])
+    assert [r.token_id for r in res] == x.argmax(1).tolist() and a.token_id == res[0].token_id
+
+
 def test_sample_batch_requires_uniforms_for_sampled_rows():
     x = torch.randn(2, 100).cuda()
     with pytest.raises(ValueError):
