@@ -262,8 +262,8 @@ def engine_step_us(device, batches=(1, 64, 256), calls=100):
     """Host wall time of one engine-shaped step (``klsample.engine.BatchedStep``): B
     requests with the headline row parameters, fp32 logits [B, 151936] on the GPU and
     2048-token device histories that grow by the sampled token each step.  One step is
-    the uniform draws, the parameter and range upload, the launch, the download of the
-    results and the ``SampleResult`` objects."""
+    the uniforms, the parameter and range hand-over, the launch, the wait and the
+    row-aligned result arrays with the stop flags (``BatchedStep.run``)."""
     import torch
     from klsample import Sampler, SamplingParams
     from klsample.engine import BatchedStep, DeviceHistory
@@ -281,11 +281,11 @@ def engine_step_us(device, batches=(1, 64, 256), calls=100):
         step = BatchedStep(device, hist)
         rids = list(range(B))
         for _ in range(10):
-            step.sample(rids, samplers, logits)
+            step.run(rids, samplers, logits)
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         for _ in range(calls):
-            step.sample(rids, samplers, logits)
+            step.run(rids, samplers, logits)
         out[f'b{B}'] = round((time.perf_counter() - t0) * 1e6 / calls, 1)
         del hist, step, logits
     return out

@@ -129,18 +129,36 @@ def load(path: Path | str | None = None) -> ctypes.CDLL:
 _hip = None
 
 
+def hip() -> ctypes.CDLL:
+    """The HIP runtime the process (torch) already has loaded, for the few calls made
+    here directly."""
+    global _hip
+    if _hip is None:
+        h = ctypes.CDLL('libamdhip64.so')
+        h.hipHostGetDevicePointer.restype = ctypes.c_int
+        h.hipHostGetDevicePointer.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_void_p, ctypes.c_uint]
+        h.hipStreamSynchronize.restype = ctypes.c_int
+        h.hipStreamSynchronize.argtypes = [ctypes.c_void_p]
+        h.hipGetErrorString.restype = ctypes.c_char_p
+        h.hipGetErrorString.argtypes = [ctypes.c_int]
+        _hip = h
+    return _hip
+
+
 def mapped_pointer(host_ptr: int) -> int | None:
     """The device's address of pinned host memory (``hipHostGetDevicePointer``), or
     None if the runtime does not map it for the device."""
-    global _hip
-    if _hip is None:
-        _hip = ctypes.CDLL('libamdhip64.so')
-        _hip.hipHostGetDevicePointer.restype = ctypes.c_int
-        _hip.hipHostGetDevicePointer.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_void_p, ctypes.c_uint]
     dev = ctypes.c_void_p()
-    if _hip.hipHostGetDevicePointer(ctypes.byref(dev), ctypes.c_void_p(host_ptr), 0) != 0 or not dev.value:
+    if hip().hipHostGetDevicePointer(ctypes.byref(dev), ctypes.c_void_p(host_ptr), 0) != 0 or not dev.value:
         return None
     return dev.value
+
+
+def stream_synchronize(stream: int) -> None:
+    """Wait for the work enqueued on a raw hipStream_t (0: the null stream)."""
+    e = hip().hipStreamSynchronize(stream)
+    if e != 0:
+        raise KLSampleError(ERR_HIP, 'hipStreamSynchronize: ' + hip().hipGetErrorString(e).decode())
 
 
 def last_error(lib: ctypes.CDLL) -> str:

@@ -157,20 +157,38 @@ def as_batch(logits, rids) -> torch.Tensor:
     return torch.stack(rows)
 
 
+@dataclass
+class StepOutput:
+    """One step's results, row-aligned: host arrays (copies)."""
+
+    tokens: np.ndarray          # int64 [B]
+    logprobs: np.ndarray        # float32 [B]
+    top_ids: np.ndarray         # int32 [B, N]
+    top_logprobs: np.ndarray    # float32 [B, N]
+    stopped: np.ndarray         # bool [B]: the token is one of the row's stop ids
+    counts: list                # top-N entries each row asked for
+
+
 class BatchedStep:
     """One sampling call for all rows of a device-resident ``[B, V]`` logits tensor.
 
     Row ``b`` is sampled with ``samplers[b]`` (its parameters and its own uniform stream)
     and, given a :class:`DeviceHistory`, with the device history of request ``rids[b]``,
     to which the library appends the sampled token.  The results equal ``B`` separate
-    ``Sampler.sample`` calls with ``history = prompt + generated``."""
+    ``Sampler.sample`` calls with ``history = prompt + generated``.
+
+    While a set of rows stays the same from step to step, the step holds each sampled
+    request's pending uniforms (taken from its Sampler a block at a time, handed back
+    when the set changes or on :meth:`release`), so a step reads its uniforms with one
+    array gather."""
 
     def __init__(self, device, history: DeviceHistory | None = None):
         self.runner = DeviceRunner(torch.device(device))
         self.device = self.runner.device
         self.history = history
         self.records = {}       # id(sampler) -> (sampler, row record)
-        self.key = None         # the last call's (samplers, rids, vocab) identity
+        self.key = None         # the current set's (samplers, rids, vocab) identity
+        self.sampled = []
 
     def _record(self, s: Sampler) -> np.ndarray:
         hit = self.records.get(id(s))
@@ -178,21 +196,41 @@ class BatchedStep:
             hit = self.records[id(s)] = (s, row_record(s.params))
         return hit[1]
 
-    def forget(self, sampler: Sampler) -> None:
-        self.records.pop(id(sampler), None)
+    def release(self) -> None:
+        """Hand the pending uniforms back to their samplers."""
+        for i, s in enumerate(self.sampled):
+            s.return_uniforms(self.device, self.U[i, self.pos[i]:self.lim[i]])
+        self.sampled = []
         self.key = None
 
+    def forget(self, sampler: Sampler) -> None:
+        self.release()
+        self.records.pop(id(sampler), None)
+
+    def _take(self, i: int) -> None:
+        blk = self.sampled[i].take_uniforms(self.device)
+        self.U[i, :blk.size] = blk
+        self.pos[i], self.lim[i] = 0, blk.size
+
     def _compose(self, rids, samplers, V: int) -> None:
+        self.release()
         self.rows = np.concatenate([self._record(s) for s in samplers])
         self.sampled_idx = np.array([b for b, s in enumerate(samplers) if s.params.temperature != 0], dtype=np.int64)
         self.sampled = [samplers[b] for b in self.sampled_idx.tolist()]
+        n = len(self.sampled)
+        self.U = np.zeros((n, 64), dtype=np.float32)
+        self.pos = np.zeros(n, dtype=np.int64)
+        self.lim = np.zeros(n, dtype=np.int64)
+        self.ar = np.arange(n)
+        for i in range(n):
+            self._take(i)
         self.max_top_k = max_top_k_of([s.params for s in samplers], V)
         self.N = min(max(s.params.logprobs for s in samplers), _lib.MAX_LOGPROBS)
         self.counts = [min(s.params.logprobs, V, self.N) for s in samplers]
-        self.stops = [s.params.stop_token_ids for s in samplers]
+        self.stop_rows = [(b, s.params.stop_token_ids) for b, s in enumerate(samplers) if s.params.stop_token_ids]
         self.slots = self.history.slots(rids) if self.history is not None else None
 
-    def sample(self, rids, samplers, logits: torch.Tensor) -> list[SampleResult]:
+    def run(self, rids, samplers, logits: torch.Tensor) -> StepOutput:
         if logits.dim() != 2 or not logits.is_floating_point():
             raise ValueError('logits must be a floating [batch, vocab] tensor')
         B, V = logits.shape
@@ -209,8 +247,10 @@ class BatchedStep:
             self.key = key
         rows, N = self.rows, self.N
         if self.sampled:
-            dev = self.device
-            rows['uniform'][self.sampled_idx] = [s.next_uniform(dev) for s in self.sampled]
+            for i in np.flatnonzero(self.pos == self.lim).tolist():
+                self._take(i)
+            rows['uniform'][self.sampled_idx] = self.U[self.ar, self.pos]
+            self.pos += 1
         if hist is not None:
             ranges = hist.prepare(self.slots)
             arena = hist.arena.data_ptr()
@@ -219,9 +259,19 @@ class BatchedStep:
             hist.advance(self.slots)
         else:
             out = self.runner.run_packed(logits, rows, self.max_top_k, N)
-        tokens, lps, tids, tlps = (x.tolist() for x in out[:4])
-        return [SampleResult(t, lp, tuple(zip(ti[:n], tl[:n])), t in stop)
-                for t, lp, ti, tl, n, stop in zip(tokens, lps, tids, tlps, self.counts, self.stops)]
+        tokens = out[0].copy()
+        stopped = np.zeros(B, dtype=bool)
+        for b, stop in self.stop_rows:
+            stopped[b] = int(tokens[b]) in stop
+        return StepOutput(tokens, out[1].copy(), out[2].copy(), out[3].copy(), stopped, self.counts)
+
+    def sample(self, rids, samplers, logits: torch.Tensor) -> list[SampleResult]:
+        """:meth:`run` as one ``SampleResult`` per row."""
+        o = self.run(rids, samplers, logits)
+        tids, tlps = o.top_ids.tolist(), o.top_logprobs.tolist()
+        return [SampleResult(t, lp, tuple(zip(ti[:n], tl[:n])), st)
+                for t, lp, ti, tl, n, st in zip(o.tokens.tolist(), o.logprobs.tolist(), tids, tlps, o.counts,
+                                                o.stopped.tolist())]
 
 
 @dataclass(frozen=True)
@@ -296,13 +346,15 @@ class SamplingLoop:
         for rid in rids:
             if self.state.get(rid) != expect:
                 raise ValueError(f'request {rid!r} is not in the {expect} state')
-        results = self.sampling.sample(list(rids), [self.samplers[r] for r in rids], as_batch(logits, rids))
-        for rid, res in zip(rids, results):
-            self.generated[rid].append(res.token_id)
+        o = self.sampling.run(list(rids), [self.samplers[r] for r in rids], as_batch(logits, rids))
+        tids, tlps = o.top_ids.tolist(), o.top_logprobs.tolist()
+        for rid, token, lp, ti, tl, n, stopped in zip(rids, o.tokens.tolist(), o.logprobs.tolist(), tids, tlps,
+                                                      o.counts, o.stopped.tolist()):
+            self.generated[rid].append(token)
             self.state[rid] = 'decode'
-            self.events[rid].append(TokenEvent(rid, res.token_id, res.logprob, res.top_logprobs))
-            if res.stopped or len(self.generated[rid]) >= self.max_tokens[rid]:
-                self._finish(rid, 'stop' if res.stopped else 'length')
+            self.events[rid].append(TokenEvent(rid, token, lp, tuple(zip(ti[:n], tl[:n]))))
+            if stopped or len(self.generated[rid]) >= self.max_tokens[rid]:
+                self._finish(rid, 'stop' if stopped else 'length')
 
     def step(self, decode_rids=(), decode_logits=None, prefill_rids=(), prefill_logits=None) -> None:
         try:

@@ -121,7 +121,10 @@ class DeviceRunner:
         if not torch.cuda.is_available():
             raise RuntimeError('klsample runs on a ROCm GPU; no GPU is visible to torch')
         self.device = torch.device(device)
+        self.index = self.device.index if self.device.index is not None else torch.cuda.current_device()
         self.lib = _lib.load()
+        self.layouts = {}        # call shape -> record and output views (see _layout)
+        self.generation = 0      # bumped whenever a buffer is replaced
         self.workspace = None
         self.workspace_bytes = 0
         self.stage_dev = None
@@ -134,7 +137,9 @@ class DeviceRunner:
         if self.workspace_bytes >= nbytes:
             return
         nbytes = _align(max(nbytes, int(self.workspace_bytes * 1.25)), 1 << 20)
-        ws = torch.empty(nbytes + 256, dtype=torch.uint8, device=self.device)
+        self.generation += 1
+        with torch.inference_mode(False):   # ordinary tensors: writable in and out of inference mode
+            ws = torch.empty(nbytes + 256, dtype=torch.uint8, device=self.device)
         base = ws.data_ptr()
         offset = (-base) % 256
         self.workspace = ws
@@ -147,22 +152,24 @@ class DeviceRunner:
         if self.stage_dev is not None and self.stage_dev.numel() >= nbytes:
             return
         n = _align(max(nbytes, 4096), 4096)
-        self.stage_dev = torch.empty(n, dtype=torch.uint8, device=self.device)
-        self.stage_host = torch.empty(n, dtype=torch.uint8, pin_memory=True)
+        with torch.inference_mode(False):
+            self.stage_dev = torch.empty(n, dtype=torch.uint8, device=self.device)
+            self.stage_host = torch.empty(n, dtype=torch.uint8, pin_memory=True)
 
     def _ensure_out(self, nbytes: int) -> None:
         if self.out_host is not None and self.out_host.numel() >= nbytes:
             return
         n = _align(max(nbytes, 4096), 4096)
-        self.out_host = torch.empty(n, dtype=torch.uint8, pin_memory=True)
-        # the kernels write the outputs straight into this pinned buffer when the device
-        # can address it; otherwise into a device twin copied back after the launch
-        mapped = _lib.mapped_pointer(self.out_host.data_ptr())
-        self.out_dev = None if mapped is not None else torch.empty(n, dtype=torch.uint8, device=self.device)
+        self.generation += 1
+        with torch.inference_mode(False):
+            self.out_host = torch.empty(n, dtype=torch.uint8, pin_memory=True)
+            # the kernels write the outputs straight into this pinned buffer when the
+            # device can address it; otherwise into a device twin copied back
+            mapped = _lib.mapped_pointer(self.out_host.data_ptr())
+            self.out_dev = None if mapped is not None else torch.empty(n, dtype=torch.uint8, device=self.device)
         self.out_ptr = mapped if mapped is not None else self.out_dev.data_ptr()
 
     # -- one call ------------------------------------------------------------------------
-    @torch.inference_mode()   # the buffers may have been made as inference tensors by an earlier call
     def run(self, logits: torch.Tensor, params_list, histories, uniforms, num_logprobs: int, *,
             options: int = 0, want_probs: bool = False, want_info: bool = False) -> BatchOutput:
         """Sample every row of ``logits`` ([B, V] on this device) and wait for the result."""
@@ -184,35 +191,80 @@ class DeviceRunner:
         return BatchOutput(tokens.copy(), logprobs.copy(), top_ids.copy(), top_lp.copy(),
                            info.copy() if info is not None else None, probs, V)
 
-    @torch.inference_mode()
+    def _layout(self, key):
+        """Library call record and output views of one call shape (built once per shape
+        and buffer generation; a call then sets only its pointers)."""
+        B, V, dt, max_top_k, N, want_info, options, row_stride = key
+        self._ensure_workspace(_lib.workspace_size(B, V, dt, max_top_k, N), self._stream())
+        p_lp = _align(8 * B)
+        p_tid = _align(p_lp + 4 * B)
+        p_tlp = _align(p_tid + 4 * B * N)
+        p_inf = _align(p_tlp + 4 * B * N)
+        out_bytes = _align(p_inf + (_lib.ROW_INFO_DTYPE.itemsize * B if want_info else 0))
+        self._ensure_out(out_bytes)
+        batch = _lib.Batch()
+        batch.row_stride = row_stride
+        batch.dtype, batch.batch, batch.vocab, batch.num_logprobs, batch.max_top_k = dt, B, V, N, max_top_k
+        batch.options = options
+        obase = self.out_ptr
+        batch.token_ids = obase
+        batch.logprobs = obase + p_lp
+        batch.top_ids = obase + p_tid if N else None
+        batch.top_logprobs = obase + p_tlp if N else None
+        batch.row_info = obase + p_inf if want_info else None
+        batch.workspace = self.workspace_ptr
+        batch.workspace_bytes = self.workspace_bytes
+        h = self.out_host.numpy()
+        views = (h[:8 * B].view(np.int64), h[p_lp:p_lp + 4 * B].view(np.float32),
+                 h[p_tid:p_tid + 4 * B * N].view(np.int32).reshape(B, N),
+                 h[p_tlp:p_tlp + 4 * B * N].view(np.float32).reshape(B, N),
+                 h[p_inf:p_inf + _lib.ROW_INFO_DTYPE.itemsize * B].view(_lib.ROW_INFO_DTYPE) if want_info else None)
+        lay = (self.generation, batch, ctypes.byref(batch), views, out_bytes)
+        self.layouts[key] = lay
+        return lay
+
+    def _stream(self) -> int:
+        return torch._C._cuda_getCurrentRawStream(self.index)
+
     def run_packed(self, logits: torch.Tensor, rows: np.ndarray, max_top_k: int, N: int, *,
                    offsets: np.ndarray | None = None, ids: np.ndarray | None = None, ids_ptr: int | None = None,
                    append_ptr: int | None = None, options: int = 0, want_probs: bool = False,
-                   want_info: bool = False):
+                   want_info: bool = False, host_params: bool | None = None):
         """One library call on packed rows (``klsample_row_params`` records) and wait.
 
-        ``offsets`` are the history offsets (CSR, or begin/end pairs with
-        ``OPT_HISTORY_PAIRS``) into ``ids`` (host, uploaded with the call) or into device
-        ids at ``ids_ptr``; ``append_ptr`` is ``history_append``.  Up to
-        ``HOST_PARAMS_MAX_BATCH`` rows travel in the kernel arguments (nothing is
-        uploaded without host ids).  Returns host views of tokens, logprobs, top ids, top
-        logprobs and row info (valid until the next call on this runner) and the device
-        probabilities."""
+        ``logits`` is ``[B, V]`` (or one ``[V]`` row).  ``offsets`` are the history
+        offsets (CSR, or begin/end pairs with ``OPT_HISTORY_PAIRS``) into ``ids`` (host,
+        uploaded with the call) or into device ids at ``ids_ptr``; ``append_ptr`` is
+        ``history_append``.  Up to ``HOST_PARAMS_MAX_BATCH`` rows hand their parameters
+        and offsets over in host memory (carried in the kernel arguments: nothing is
+        uploaded without host ids); ``host_params=False`` stages them as a larger batch's
+        are.  Returns host views of tokens, logprobs, top ids, top logprobs and row info
+        (valid until the next call on this runner) and the device probabilities."""
         if logits.dtype not in _DTYPES:
             logits = logits.float()
-        B, V = logits.shape
-        # rows must not overlap (a size-1 dimension may carry any stride)
-        if logits.stride(1) != 1 or (B > 1 and logits.stride(0) < V):
-            logits = logits.contiguous()
-        stream = torch.cuda.current_stream(self.device)
-        sptr = stream.cuda_stream
-        dt = _DTYPES[logits.dtype]
-        self._ensure_workspace(_lib.workspace_size(B, V, dt, max_top_k, N), sptr)
-        batch = _lib.Batch()
-        host_params = B <= _lib.HOST_PARAMS_MAX_BATCH
+        if logits.dim() == 1:
+            B, V = 1, logits.shape[0]
+            if logits.stride(0) != 1:
+                logits = logits.contiguous()
+            row_stride = V
+        else:
+            B, V = logits.shape
+            # rows must not overlap (a size-1 dimension may carry any stride)
+            if logits.stride(1) != 1 or (B > 1 and logits.stride(0) < V):
+                logits = logits.contiguous()
+            row_stride = logits.stride(0) if B > 1 else V
+        if host_params is None:
+            host_params = B <= _lib.HOST_PARAMS_MAX_BATCH
+        if host_params:
+            options |= _lib.OPT_HOST_PARAMS
+        key = (B, V, _DTYPES[logits.dtype], max_top_k, N, want_info, options, row_stride)
+        lay = self.layouts.get(key)
+        if lay is None or lay[0] != self.generation:
+            lay = self._layout(key)
+        _, batch, ref, views, out_bytes = lay
         # one host-to-device copy, if any: params | offsets (larger batches) | ids
-        o_off = _align(rows.nbytes) if not host_params else 0
-        o_ids = _align(o_off + offsets.nbytes) if offsets is not None and not host_params else o_off
+        o_off = 0 if host_params else _align(rows.nbytes)
+        o_ids = o_off if offsets is None or host_params else _align(o_off + offsets.nbytes)
         stage_bytes = _align(o_ids + (ids.nbytes if ids is not None else 0))
         if stage_bytes:
             self._ensure_stage(stage_bytes)
@@ -226,57 +278,28 @@ class DeviceRunner:
             self.stage_dev[:stage_bytes].copy_(self.stage_host[:stage_bytes], non_blocking=True)
             dbase = self.stage_dev.data_ptr()
         if host_params:
-            options |= _lib.OPT_HOST_PARAMS
             batch.params = rows.ctypes.data
-            if offsets is not None:
-                batch.history_offsets = offsets.ctypes.data
+            batch.history_offsets = offsets.ctypes.data if offsets is not None else None
         else:
             batch.params = dbase
-            if offsets is not None:
-                batch.history_offsets = dbase + o_off
-        if ids is not None:
-            batch.history_ids = dbase + o_ids
-        elif ids_ptr is not None:
-            batch.history_ids = ids_ptr
+            batch.history_offsets = dbase + o_off if offsets is not None else None
+        batch.history_ids = dbase + o_ids if ids is not None else ids_ptr
         batch.history_append = append_ptr
-
-        # outputs: tokens | logprobs | top ids | top logprobs | info
-        p_lp = _align(8 * B)
-        p_tid = _align(p_lp + 4 * B)
-        p_tlp = _align(p_tid + 4 * B * N)
-        p_inf = _align(p_tlp + 4 * B * N)
-        out_bytes = _align(p_inf + (_lib.ROW_INFO_DTYPE.itemsize * B if want_info else 0))
-        self._ensure_out(out_bytes)
-        obase = self.out_ptr
-        probs = torch.empty((B, V), dtype=torch.float32, device=self.device) if want_probs else None
-
         batch.logits = logits.data_ptr()
-        batch.row_stride = logits.stride(0) if B > 1 else V
-        batch.dtype = dt
-        batch.batch = B
-        batch.vocab = V
-        batch.num_logprobs = N
-        batch.max_top_k = max_top_k
-        batch.options = options
-        batch.token_ids = obase
-        batch.logprobs = obase + p_lp
-        batch.top_ids = obase + p_tid if N else None
-        batch.top_logprobs = obase + p_tlp if N else None
-        batch.probs = probs.data_ptr() if probs is not None else None
-        batch.row_info = obase + p_inf if want_info else None
-        batch.workspace = self.workspace_ptr
-        batch.workspace_bytes = self.workspace_bytes
-        _lib.check(self.lib, self.lib.klsample_run(ctypes.byref(batch), ctypes.c_void_p(sptr)))
+        probs = None
+        if want_probs:
+            probs = torch.empty((B, V), dtype=torch.float32, device=self.device)
+            batch.probs = probs.data_ptr()
+        else:
+            batch.probs = None
+        sptr = self._stream()
+        status = self.lib.klsample_run(ref, sptr)
+        if status:
+            _lib.check(self.lib, status)
         if self.out_dev is not None:
             self.out_host[:out_bytes].copy_(self.out_dev[:out_bytes], non_blocking=True)
-        stream.synchronize()
-        h = self.out_host.numpy()
-        tokens = h[:8 * B].view(np.int64)
-        logprobs = h[p_lp:p_lp + 4 * B].view(np.float32)
-        top_ids = h[p_tid:p_tid + 4 * B * N].view(np.int32).reshape(B, N)
-        top_lp = h[p_tlp:p_tlp + 4 * B * N].view(np.float32).reshape(B, N)
-        info = h[p_inf:p_inf + _lib.ROW_INFO_DTYPE.itemsize * B].view(_lib.ROW_INFO_DTYPE) if want_info else None
-        return tokens, logprobs, top_ids, top_lp, info, probs
+        _lib.stream_synchronize(sptr)
+        return views + (probs,)
 
 
 _local = threading.local()

@@ -20,6 +20,7 @@ from __future__ import annotations
 import math
 from dataclasses import dataclass
 
+import numpy as np
 import torch
 
 from . import _lib
@@ -102,6 +103,24 @@ class Sampler:
         block[1] += 1
         return u
 
+    def take_uniforms(self, device) -> np.ndarray:
+        """Hand the rest of the current block of uniforms (a fresh block if it is spent)
+        to a caller that consumes them in order, as fp32 values.  Until they are returned
+        (:meth:`return_uniforms`), the request's draws belong to that caller."""
+        key = str(device)
+        block = self.uniforms.get(key)
+        if block is None or block[1] == len(block[0]):
+            out = torch.rand(_UNIFORM_BLOCK, generator=self._generator(device)).numpy()
+        else:
+            out = np.asarray(block[0][block[1]:], dtype=np.float32)
+        self.uniforms[key] = [[], 0]
+        return out
+
+    def return_uniforms(self, device, rest) -> None:
+        """Give back the unconsumed part of what :meth:`take_uniforms` handed out; the
+        next draws continue from its first value."""
+        self.uniforms[str(device)] = [[float(u) for u in rest], 0]
+
     @torch.inference_mode()
     def sample(self, logits: torch.Tensor, history=()) -> SampleResult:
         if logits.ndim != 1 or not logits.is_floating_point():
@@ -121,7 +140,7 @@ class Sampler:
         rec['uniform'][0] = u
         N = min(p.logprobs, _lib.MAX_LOGPROBS)
         top_k = min(int(p.top_k), V) if p.temperature != 0 and p.top_k > 0 else 0
-        tokens, lps, tids, tlps, _, _ = runner_for(device).run_packed(logits.unsqueeze(0), rec, top_k, N)
+        tokens, lps, tids, tlps, _, _ = runner_for(device).run_packed(logits, rec, top_k, N)
         token = int(tokens[0])
         n = min(p.logprobs, V, N)
         return SampleResult(token, float(lps[0]), tuple(zip(tids[0, :n].tolist(), tlps[0, :n].tolist())),

@@ -177,3 +177,21 @@ def test_workloads_match_the_committed_digests(name):
     (tests/golden/make_workload_digests.py); the GPU tests repeat this on the GPU host."""
     want = json.loads(DIGESTS.read_text())[name]
     assert workloads.digest(workloads.make(name)) == want
+
+
+def test_uniforms_taken_in_blocks_and_returned_keep_the_stream():
+    """A batched step takes a request's pending uniforms and hands back what it did not
+    use: the request's stream of uniforms is unchanged by that."""
+    s = Sampler(SamplingParams(temperature=1.0, seed=5))
+    g = torch.Generator().manual_seed(5)
+    want = [float(torch.rand((), generator=g)) for _ in range(200)]
+    got = [s.next_uniform('cpu') for _ in range(3)]
+    blk = s.take_uniforms('cpu')
+    assert blk.dtype == np.float32 and blk.size == 61
+    got += blk[:10].tolist()
+    s.return_uniforms('cpu', blk[10:])
+    got += [s.next_uniform('cpu') for _ in range(60)]
+    blk = s.take_uniforms('cpu')          # the rest of the block the draws above started
+    got += blk.tolist()
+    got += [s.next_uniform('cpu') for _ in range(10)]
+    assert got == want[:len(got)]

@@ -110,6 +110,35 @@ def test_repeated_calls_are_deterministic():
         assert np.array_equal(o.logprobs, outs[0].logprobs)
 
 
+@pytest.mark.parametrize('name,rows', [('cpu_reference_b8', 8), ('mixed_b64', 8), ('mixed_b64', 3),
+                                       ('latency_b1', 1), ('latency_b1_greedy', 1), ('tie_stress_b1024', 5)])
+def test_inline_parameters_equal_staged_parameters(name, rows):
+    """Up to eight rows may hand their parameters and history offsets over in the kernel
+    arguments (KLSAMPLE_OPT_HOST_PARAMS) instead of device memory.  Both give identical
+    outputs, on either row path; the output buffer is overwritten with garbage before
+    every call, so a call that left a row unwritten would show."""
+    from klsample.runner import pack_rows
+    say(f'inline parameters {name}[:{rows}]')
+    w = workloads.make(name, batch=rows, num_logprobs=5)
+    logits = w.logits.to(DEV)
+    packed, offsets, ids, kmax = pack_rows(w.params, w.histories, w.uniforms, w.vocab)
+    r = runner_for(DEV)
+    outs = []
+    for host, options in ((False, 0), (True, 0), (True, 0), (False, 0),
+                          (False, _lib.OPT_FORCE_DENSE), (True, _lib.OPT_FORCE_DENSE)):
+        if r.out_host is not None:
+            r.out_host.numpy()[:] = 0xA5
+        o = r.run_packed(logits, packed, kmax, 5, offsets=offsets if ids.size else None,
+                         ids=ids if ids.size else None, options=options, want_info=True, host_params=host)
+        outs.append((options, [x.copy() for x in o[:4]], o[4].copy()))
+    for options, arrays, info in outs:
+        base = next(x for x in outs if x[0] == options)
+        for a, b in zip(arrays, base[1]):
+            assert np.array_equal(a, b)
+        assert info.tobytes() == base[2].tobytes()
+    assert (outs[-1][2]['path'] == 1).all()
+
+
 # ---- vectors written by the reference sampler ----------------------------------------------
 
 CASES = golden_cases()
