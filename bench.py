@@ -291,6 +291,43 @@ def engine_step_us(device, batches=(1, 64, 256), calls=100):
     return out
 
 
+def lmhead_us(device, batches=(1, 8, 64, 256), calls=200):
+    """Host wall per call (one synchronisation each) of the fused LM head + sampling call
+    (``klsample_lmhead_run``) against torch's bf16 ``hidden @ weight.T`` followed by
+    ``klsample_run``, at V = 151,936 and d = 1,024 (Qwen3-0.6B's LM head), greedy and
+    top-k 50 rows, random bf16 weights and hidden states."""
+    import numpy as np
+    import torch
+    from klsample import SamplingParams
+    from klsample.lmhead import lmhead_sample
+    from klsample.runner import runner_for
+    V, d = 151936, 1024
+    g = torch.Generator(device=device).manual_seed(0)
+    weight = (torch.randn(V, d, generator=g, device=device) * (3.0 / d ** 0.5)).bfloat16()
+    r = runner_for(device)
+
+    def wall(fn):
+        for _ in range(10):
+            fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(calls):
+            fn()
+        torch.cuda.synchronize()
+        return round((time.perf_counter() - t0) * 1e6 / calls, 1)
+
+    out = {}
+    for B in batches:
+        hidden = torch.randn(B, d, generator=g, device=device).bfloat16()
+        uni = np.full(B, 0.5, np.float32)
+        for kind, p in (('greedy', SamplingParams()), ('top_k50', SamplingParams(temperature=0.8, top_k=50, seed=1))):
+            params = [p] * B
+            out[f'b{B}_{kind}'] = {
+                'fused': wall(lambda: lmhead_sample(hidden, weight, params, None, uni)),
+                'matmul_then_sample': wall(lambda: r.run((hidden @ weight.T).float(), params, None, uni, 0))}
+    return out
+
+
 # the other configurations of the sampling path, each timed at its own shape (device time
 # per call, inputs resident): workload name, timed calls, warm-up calls
 OTHER_CONFIGS = (
@@ -510,6 +547,7 @@ def main():
     ap.add_argument('--summarize-stats', metavar='DIR')
     ap.add_argument('--summarize-pmc', nargs=2, metavar=('FETCH_DIR', 'WRITE_DIR'))
     ap.add_argument('--summarize-parity', metavar='JSONL')
+    ap.add_argument('--lmhead', action='store_true', help='fused LM head + sampling against matmul + sampling')
     ap.add_argument('--command', nargs='*', default=[])
     args = ap.parse_args()
 
@@ -534,6 +572,9 @@ def main():
         return 1
     device = torch.device('cuda', 0)
     torch.cuda.set_device(device)
+    if args.lmhead:
+        print(json.dumps({'lmhead_call_wall_us': lmhead_us(device)}), flush=True)
+        return 0
 
     if args.profile_run:
         res = Resident(HEADLINE, device)

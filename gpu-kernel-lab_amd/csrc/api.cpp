@@ -54,7 +54,8 @@ int check_sizes(int32_t batch, int32_t vocab, int32_t dtype, int32_t max_top_k, 
 
 namespace kls {
 
-bool make_plan(int32_t batch, int32_t vocab, int32_t dtype, int32_t max_top_k, int32_t num_logprobs, Plan *p) {
+bool make_plan(int32_t batch, int32_t vocab, int32_t dtype, int32_t max_top_k, int32_t num_logprobs, Plan *p,
+               int32_t elems) {
     // Elements per thread: 32, the largest built variant.  Larger chunks amortise each
     // workgroup's fixed work (history table, candidate bound) in the streaming pass and
     // leave fewer chunk summaries and candidates for the row combine, which matters most
@@ -70,6 +71,7 @@ bool make_plan(int32_t batch, int32_t vocab, int32_t dtype, int32_t max_top_k, i
         for (int i = 0; i < ncands; ++i)
             if (cands[i] == want) e = want;
     }
+    if (elems > 0) e = elems;
     p->elems = e;
     p->chunk = kThreads * e;
     p->chunks = (vocab + p->chunk - 1) / p->chunk;
@@ -136,7 +138,7 @@ namespace {
 
 // Validates everything of a call but its workspace and fills the kernel arguments (the
 // workspace pointers excepted).  Host only: no HIP call.
-int prepare(const klsample_batch *b, kls::Plan *plan, kls::Args *args) {
+int prepare(const klsample_batch *b, kls::Plan *plan, kls::Args *args, int32_t elems = 0) {
     if (b == nullptr) return fail(KLSAMPLE_ERR_INVALID_ARGUMENT, "batch must not be NULL");
     int st = check_sizes(b->batch, b->vocab, b->dtype, b->max_top_k, b->num_logprobs);
     if (st != KLSAMPLE_OK) return st;
@@ -161,7 +163,7 @@ int prepare(const klsample_batch *b, kls::Plan *plan, kls::Args *args) {
         return fail(KLSAMPLE_ERR_INVALID_ARGUMENT, "history_append needs KLSAMPLE_OPT_HISTORY_PAIRS");
     if (b->history_append != nullptr && b->history_offsets == nullptr)
         return fail(KLSAMPLE_ERR_INVALID_ARGUMENT, "history_append needs history ranges (history_offsets)");
-    if (!kls::make_plan(b->batch, b->vocab, b->dtype, b->max_top_k, b->num_logprobs, plan))
+    if (!kls::make_plan(b->batch, b->vocab, b->dtype, b->max_top_k, b->num_logprobs, plan, elems))
         return fail(KLSAMPLE_ERR_INVALID_ARGUMENT, "batch * chunks exceeds the grid limit");
 
     const size_t esize = b->dtype == KLSAMPLE_FLOAT32 ? 4 : 2;
@@ -236,6 +238,54 @@ int klsample_run(const klsample_batch *b, void *stream) {
         return fail(KLSAMPLE_ERR_WORKSPACE, "workspace too small: %zu bytes given, %zu needed", b->workspace_bytes,
                     plan.total);
     return launch(b, plan, a, b->workspace, stream);
+}
+
+int klsample_lmhead_workspace_size(int32_t batch, int32_t vocab, int32_t max_top_k, int32_t num_logprobs,
+                                   size_t *bytes) {
+    if (bytes == nullptr) return fail(KLSAMPLE_ERR_INVALID_ARGUMENT, "bytes must not be NULL");
+    const int st = check_sizes(batch, vocab, KLSAMPLE_FLOAT32, max_top_k, num_logprobs);
+    if (st != KLSAMPLE_OK) return st;
+    kls::Plan plan;
+    if (!kls::make_plan(batch, vocab, KLSAMPLE_FLOAT32, max_top_k, num_logprobs, &plan, kls::kHeadElems))
+        return fail(KLSAMPLE_ERR_INVALID_ARGUMENT, "batch * chunks exceeds the grid limit");
+    *bytes = plan.total;
+    return ok();
+}
+
+int klsample_lmhead_run(const klsample_batch *b, const klsample_lmhead *h, void *stream) {
+    if (h == nullptr) return fail(KLSAMPLE_ERR_INVALID_ARGUMENT, "head must not be NULL");
+    if (h->hidden == nullptr || h->weight == nullptr)
+        return fail(KLSAMPLE_ERR_INVALID_ARGUMENT, "hidden and weight must not be NULL");
+    if (h->dim < 32 || h->dim % 32 != 0)
+        return fail(KLSAMPLE_ERR_INVALID_ARGUMENT, "dim (%d) must be a positive multiple of 32", h->dim);
+    if ((((uintptr_t)h->hidden | (uintptr_t)h->weight) & 15u) != 0)
+        return fail(KLSAMPLE_ERR_INVALID_ARGUMENT, "hidden and weight must be 16-byte aligned");
+    if (b != nullptr && (b->dtype != KLSAMPLE_FLOAT32 || b->row_stride != b->vocab))
+        return fail(KLSAMPLE_ERR_INVALID_ARGUMENT, "the LM-head path writes fp32 logits with row_stride == vocab");
+    kls::Plan plan;
+    kls::Args a;
+    const int st = prepare(b, &plan, &a, kls::kHeadElems);
+    if (st != KLSAMPLE_OK) return st;
+    if (b->workspace == nullptr) return fail(KLSAMPLE_ERR_WORKSPACE, "workspace must not be NULL");
+    if (((uintptr_t)b->workspace & 255u) != 0) return fail(KLSAMPLE_ERR_WORKSPACE, "workspace must be 256-byte aligned");
+    if (b->workspace_bytes < plan.total)
+        return fail(KLSAMPLE_ERR_WORKSPACE, "workspace too small: %zu bytes given, %zu needed", b->workspace_bytes,
+                    plan.total);
+    a.wide_split = 0;   // one workgroup per (chunk, row block) writes the histograms too
+    unsigned char *ws = static_cast<unsigned char *>(b->workspace);
+    a.stats = reinterpret_cast<kls::ChunkStat *>(ws + plan.off_stats);
+    a.cands = reinterpret_cast<kls::Cand *>(ws + plan.off_cands);
+    a.rows = reinterpret_cast<klsample_row_info *>(ws + plan.off_rows);
+    a.ybuf = reinterpret_cast<float *>(ws + plan.off_ybuf);
+    a.hist = reinterpret_cast<unsigned long long *>(ws + plan.off_hist);
+    kls::HeadArgs head;
+    head.hidden = static_cast<const uint16_t *>(h->hidden);
+    head.weight = static_cast<const uint16_t *>(h->weight);
+    head.logits_out = static_cast<float *>(const_cast<void *>(b->logits));
+    head.dim = h->dim;
+    const hipError_t e = kls::launch_lmhead(a, head, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return fail(KLSAMPLE_ERR_HIP, "kernel launch failed: %s", hipGetErrorString(e));
+    return ok();
 }
 
 int klsample_run_noalloc(const klsample_batch *b, void *stream) {

@@ -68,8 +68,9 @@ struct Plan {
     size_t off_stats, off_cands, off_rows, off_ybuf, off_hist, total;
 };
 
+// elems > 0 pins the elements per thread (the LM-head path's chunks)
 bool make_plan(int32_t batch, int32_t vocab, int32_t dtype, int32_t max_top_k, int32_t num_logprobs,
-               Plan *plan);
+               Plan *plan, int32_t elems = 0);
 
 // Everything a kernel needs, passed by value.
 struct Args {
@@ -113,6 +114,19 @@ struct PhaseEvents {
 };
 
 hipError_t launch_sample(const Args &args, int32_t dtype, hipStream_t stream, const PhaseEvents *phases);
+
+// LM head fused with the streaming pass: logits[b][v] = bf16(sum_k hidden[b][k] * weight[v][k])
+// computed per (vocabulary chunk of kHeadChunk, block of kHeadRows rows) with bf16 MFMA,
+// materialised into `logits_out` (= Args::logits, fp32 [B][V]) and scanned from LDS.
+constexpr int kHeadElems = 4;                     // chunk = kThreads * kHeadElems vocabulary rows
+constexpr int kHeadRows = 16;                     // batch rows per workgroup (one MFMA column tile)
+struct HeadArgs {
+    const uint16_t *hidden;   // [B][dim] bf16
+    const uint16_t *weight;   // [V][dim] bf16
+    float *logits_out;        // [B][V] fp32
+    int32_t dim;              // multiple of 32
+};
+hipError_t launch_lmhead(const Args &args, const HeadArgs &head, hipStream_t stream);
 hipError_t launch_zero_fill(void *ptr, size_t bytes, hipStream_t stream);
 
 // Workspace of klsample_run_noalloc: a static device array of kScratchBytes per GPU.

@@ -3172,10 +3172,11 @@ __device__ __forceinline__ void wide_chunk(const Args &a, int row, int chunk, co
 // with no per-element branch.
 // kInline: a launch whose row parameters (and maybe history offsets) are in the kernel
 // arguments (small batches); a separate instantiation keeps the branch out of the
-// streaming pass's register budget.
-template <typename TIn, int E, bool kVec, bool kInline>
+// streaming pass's register budget.  kLds: the chunk's logits come from LDS (`lsrc`,
+// fp32, the chunk's C entries), where the LM-head kernel computed them.
+template <typename TIn, int E, bool kVec, bool kInline, bool kLds = false>
 __device__ __forceinline__ void scan_chunk(const Args &a, int row, int chunk, unsigned char *raw, ScanMisc &ms,
-                                           bool wide_only) {
+                                           bool wide_only, const float *lsrc = nullptr) {
     constexpr int VW = Loader<TIn>::VW;
     constexpr int NV = E / VW;
     constexpr int C = kThreads * E;
@@ -3258,7 +3259,8 @@ __device__ __forceinline__ void scan_chunk(const Args &a, int row, int chunk, un
 #pragma unroll
             for (int e = 0; e < VW; ++e) {
                 const int li = (v * kThreads + tid) * VW + e;
-                x[v * VW + e] = (li < cn) ? Loader<TIn>::one(src + li) : kNegInf;
+                if constexpr (kLds) x[v * VW + e] = (li < cn) ? lsrc[li] : kNegInf;
+                else x[v * VW + e] = (li < cn) ? Loader<TIn>::one(src + li) : kNegInf;
             }
         }
     }
@@ -3659,6 +3661,91 @@ __global__ __launch_bounds__(kThreads) void row_kernel(Args a) {
     row_body<TIn, E>(a, blockIdx.x, raw, cnt, ms);
 }
 
+// ---------------------------------------------------------------------------------
+// LM head fused with the streaming pass (serving/qwen_executor.py:238 computes
+// lm_head(hidden) in bf16, then the sampler reads the logits back).  Workgroup
+// (chunk, row block) multiplies its kThreads * kHeadElems vocabulary rows of the weight
+// with kHeadRows hidden rows: each wave owns 256 vocabulary rows as sixteen 16x16 tiles
+// of v_mfma_f32_16x16x32_bf16 (vocabulary along M, batch along N, 32 of the hidden
+// dimension per step, the next step's operands loaded before this step's products).
+// The fp32 sums are rounded to bf16 as the reference's bf16 output is, written to LDS
+// and to the materialised logits, and each row of the block is then scanned from LDS by
+// the streaming pass's own code.  The row kernel follows as for any call.
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+__device__ __forceinline__ float round_bf16(float x) {
+    uint32_t u = __float_as_uint(x);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return __uint_as_float(u | 0x00400000u);   // NaN stays NaN
+    u += 0x7fffu + ((u >> 16) & 1u);                                                 // nearest, ties to even
+    return __uint_as_float(u & 0xffff0000u);
+}
+
+template <bool kInline>
+__global__ __launch_bounds__(kThreads) void lmhead_kernel(Args a, HeadArgs h) {
+    constexpr int C = kThreads * kHeadElems;
+    constexpr int kTiles = C / kWaves / 16;   // 16-row vocabulary tiles per wave
+    __shared__ __attribute__((aligned(16))) float lg[kHeadRows * C];
+    __shared__ __attribute__((aligned(16))) unsigned char raw[ScanLds<kHeadElems>::value];
+    __shared__ ScanMisc ms;
+    const int chunk = (int)blockIdx.x % a.S;
+    const int r0 = ((int)blockIdx.x / a.S) * kHeadRows;
+    const int w = wave_id(), l = lane_id();
+    const int g = l >> 4, n = l & 15;          // lane group (8 of the 32 hidden entries a step), tile row / column
+    const int vwave = chunk * C + w * (C / kWaves);
+    // operand rows: vocabulary rows past V and batch rows past B read row 0 / a zero operand
+    const uint16_t *wrow[kTiles];
+#pragma unroll
+    for (int t = 0; t < kTiles; ++t) {
+        const int v = vwave + t * 16 + n;
+        wrow[t] = h.weight + (size_t)(v < a.V ? v : 0) * h.dim + 8 * g;
+    }
+    const bool hvalid = r0 + n < a.B;
+    const uint16_t *hrow = h.hidden + (size_t)(hvalid ? r0 + n : 0) * h.dim + 8 * g;
+    f32x4 acc[kTiles];
+#pragma unroll
+    for (int t = 0; t < kTiles; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const bf16x8 zero8 = {};
+    bf16x8 an[kTiles], bn;
+#pragma unroll
+    for (int t = 0; t < kTiles; ++t) an[t] = __builtin_nontemporal_load(reinterpret_cast<const bf16x8 *>(wrow[t]));
+    bn = hvalid ? *reinterpret_cast<const bf16x8 *>(hrow) : zero8;
+    for (int k0 = 0; k0 < h.dim; k0 += 32) {
+        bf16x8 ac[kTiles];
+#pragma unroll
+        for (int t = 0; t < kTiles; ++t) ac[t] = an[t];
+        const bf16x8 bc = bn;
+        if (k0 + 32 < h.dim) {
+#pragma unroll
+            for (int t = 0; t < kTiles; ++t)
+                an[t] = __builtin_nontemporal_load(reinterpret_cast<const bf16x8 *>(wrow[t] + k0 + 32));
+            bn = hvalid ? *reinterpret_cast<const bf16x8 *>(hrow + k0 + 32) : zero8;
+        }
+#pragma unroll
+        for (int t = 0; t < kTiles; ++t) acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ac[t], bc, acc[t], 0, 0, 0);
+    }
+    // tile t, lane l, entry j: vocabulary row vwave + 16t + 4g + j, batch row r0 + n
+    const int rowg = r0 + n;
+#pragma unroll
+    for (int t = 0; t < kTiles; ++t) {
+        const int vl = w * (C / kWaves) + t * 16 + 4 * g;   // within the chunk
+        const f32x4 q = {round_bf16(acc[t][0]), round_bf16(acc[t][1]), round_bf16(acc[t][2]), round_bf16(acc[t][3])};
+        *reinterpret_cast<f32x4 *>(&lg[n * C + vl]) = q;
+        const int v = chunk * C + vl;
+        if (rowg < a.B) {
+            float *o = h.logits_out + (size_t)rowg * a.V + v;
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                if (v + j < a.V) o[j] = q[j];
+        }
+    }
+    __syncthreads();
+    const int rows = min(kHeadRows, a.B - r0);
+    for (int i = 0; i < rows; ++i) {
+        scan_chunk<float, kHeadElems, false, kInline, true>(a, r0 + i, chunk, raw, ms, false, lg + i * C);
+        __syncthreads();
+    }
+}
+
 // Final probabilities: exp(s - max - log_norm) on the kept set, 0 elsewhere.
 template <typename TIn, int E>
 __global__ __launch_bounds__(kThreads) void probs_kernel(Args a) {
@@ -3720,6 +3807,16 @@ hipError_t launch_typed(const Args &a, hipStream_t s, const PhaseEvents *ph) {
 }
 
 }  // namespace
+
+hipError_t launch_lmhead(const Args &a, const HeadArgs &h, hipStream_t s) {
+    if (a.E != kHeadElems || a.wide_split) return hipErrorInvalidValue;
+    const dim3 grid((unsigned)((int64_t)a.S * ((a.B + kHeadRows - 1) / kHeadRows)));
+    if (a.inline_flags & kInlineParams) lmhead_kernel<true><<<grid, kThreads, 0, s>>>(a, h);
+    else lmhead_kernel<false><<<grid, kThreads, 0, s>>>(a, h);
+    row_kernel<float, kHeadElems><<<dim3((unsigned)a.B), kThreads, 0, s>>>(a);
+    if (a.probs) probs_kernel<float, kHeadElems><<<dim3((unsigned)((int64_t)a.B * a.S)), kThreads, 0, s>>>(a);
+    return hipGetLastError();
+}
 
 hipError_t launch_sample(const Args &a, int32_t dtype, hipStream_t s, const PhaseEvents *ph) {
     if (dtype == KLSAMPLE_FLOAT32) {

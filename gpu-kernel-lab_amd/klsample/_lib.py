@@ -38,7 +38,8 @@ MAX_BATCH = 65536
 MAX_VOCAB = 1 << 24
 
 EXPORTS = ('klsample_abi_version', 'klsample_workspace_size', 'klsample_workspace_init',
-           'klsample_run', 'klsample_run_noalloc', 'klsample_set_phase_events', 'klsample_last_error')
+           'klsample_run', 'klsample_run_noalloc', 'klsample_set_phase_events', 'klsample_last_error',
+           'klsample_lmhead_workspace_size', 'klsample_lmhead_run')
 NOALLOC_SCRATCH_BYTES = 64 << 20
 
 # klsample_row_params, 32 bytes
@@ -81,6 +82,13 @@ class Batch(ctypes.Structure):
     ]
 
 
+class LMHead(ctypes.Structure):
+    """``klsample_lmhead``."""
+
+    _fields_ = [('hidden', ctypes.c_void_p), ('weight', ctypes.c_void_p), ('dim', ctypes.c_int32),
+                ('reserved', ctypes.c_int32)]
+
+
 class KLSampleError(RuntimeError):
     """A non-zero status from the library."""
 
@@ -116,6 +124,10 @@ def load(path: Path | str | None = None) -> ctypes.CDLL:
         lib.klsample_run.argtypes = [ctypes.POINTER(Batch), ctypes.c_void_p]
         lib.klsample_run_noalloc.restype = ctypes.c_int
         lib.klsample_run_noalloc.argtypes = [ctypes.POINTER(Batch), ctypes.c_void_p]
+        lib.klsample_lmhead_workspace_size.restype = ctypes.c_int
+        lib.klsample_lmhead_workspace_size.argtypes = [ctypes.c_int32] * 4 + [ctypes.POINTER(ctypes.c_size_t)]
+        lib.klsample_lmhead_run.restype = ctypes.c_int
+        lib.klsample_lmhead_run.argtypes = [ctypes.POINTER(Batch), ctypes.POINTER(LMHead), ctypes.c_void_p]
         lib.klsample_set_phase_events.restype = ctypes.c_int
         lib.klsample_set_phase_events.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_int32]
         version = lib.klsample_abi_version()
@@ -171,6 +183,13 @@ def check(lib: ctypes.CDLL, status: int) -> None:
         if status in (ERR_INVALID_ARGUMENT, ERR_UNSUPPORTED_DTYPE):
             raise ValueError(f'klsample status {status}: {message}')
         raise KLSampleError(status, message)
+
+
+def lmhead_workspace_size(batch: int, vocab: int, max_top_k: int, num_logprobs: int) -> int:
+    lib = load()
+    out = ctypes.c_size_t(0)
+    check(lib, lib.klsample_lmhead_workspace_size(batch, vocab, max_top_k, num_logprobs, ctypes.byref(out)))
+    return int(out.value)
 
 
 def workspace_size(batch: int, vocab: int, dtype: int, max_top_k: int, num_logprobs: int) -> int:

@@ -194,8 +194,9 @@ class DeviceRunner:
     def _layout(self, key):
         """Library call record and output views of one call shape (built once per shape
         and buffer generation; a call then sets only its pointers)."""
-        B, V, dt, max_top_k, N, want_info, options, row_stride = key
-        self._ensure_workspace(_lib.workspace_size(B, V, dt, max_top_k, N), self._stream())
+        B, V, dt, max_top_k, N, want_info, options, row_stride, head = key
+        ws = _lib.lmhead_workspace_size(B, V, max_top_k, N) if head else _lib.workspace_size(B, V, dt, max_top_k, N)
+        self._ensure_workspace(ws, self._stream())
         p_lp = _align(8 * B)
         p_tid = _align(p_lp + 4 * B)
         p_tlp = _align(p_tid + 4 * B * N)
@@ -229,7 +230,7 @@ class DeviceRunner:
     def run_packed(self, logits: torch.Tensor, rows: np.ndarray, max_top_k: int, N: int, *,
                    offsets: np.ndarray | None = None, ids: np.ndarray | None = None, ids_ptr: int | None = None,
                    append_ptr: int | None = None, options: int = 0, want_probs: bool = False,
-                   want_info: bool = False, host_params: bool | None = None):
+                   want_info: bool = False, host_params: bool | None = None, head=None):
         """One library call on packed rows (``klsample_row_params`` records) and wait.
 
         ``logits`` is ``[B, V]`` (or one ``[V]`` row).  ``offsets`` are the history
@@ -239,7 +240,9 @@ class DeviceRunner:
         and offsets over in host memory (carried in the kernel arguments: nothing is
         uploaded without host ids); ``host_params=False`` stages them as a larger batch's
         are.  Returns host views of tokens, logprobs, top ids, top logprobs and row info
-        (valid until the next call on this runner) and the device probabilities."""
+        (valid until the next call on this runner) and the device probabilities.  With
+        ``head`` (a ``klsample_lmhead``), ``logits`` is the fp32 output the LM head writes
+        and the call is ``klsample_lmhead_run``."""
         if logits.dtype not in _DTYPES:
             logits = logits.float()
         if logits.dim() == 1:
@@ -257,7 +260,7 @@ class DeviceRunner:
             host_params = B <= _lib.HOST_PARAMS_MAX_BATCH
         if host_params:
             options |= _lib.OPT_HOST_PARAMS
-        key = (B, V, _DTYPES[logits.dtype], max_top_k, N, want_info, options, row_stride)
+        key = (B, V, _DTYPES[logits.dtype], max_top_k, N, want_info, options, row_stride, head is not None)
         lay = self.layouts.get(key)
         if lay is None or lay[0] != self.generation:
             lay = self._layout(key)
@@ -293,7 +296,10 @@ class DeviceRunner:
         else:
             batch.probs = None
         sptr = self._stream()
-        status = self.lib.klsample_run(ref, sptr)
+        if head is None:
+            status = self.lib.klsample_run(ref, sptr)
+        else:
+            status = self.lib.klsample_lmhead_run(ref, ctypes.byref(head), sptr)
         if status:
             _lib.check(self.lib, status)
         if self.out_dev is not None:

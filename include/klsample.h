@@ -165,6 +165,26 @@ int klsample_run_noalloc(const klsample_batch *batch, void *stream);
  * slightly slower than unrecorded ones. */
 int klsample_set_phase_events(void *const *events, int32_t count);
 
+/* LM head fused with the sampling call (prototype).  Replaces the executor's
+ * `self.model.lm_head(hidden)[:,0].float()` (serving/qwen_executor.py:238) followed by
+ * the sampler: logits[b][v] = bf16(sum_k hidden[b][k] * weight[v][k]) (fp32 sums rounded
+ * to bf16, as the reference's bf16 output), computed chunk by chunk with bf16 matrix
+ * cores and scanned for sampling while still on chip.  The logits are also written to
+ * batch->logits, which here is an OUTPUT ([batch, vocab] fp32, row_stride == vocab,
+ * dtype KLSAMPLE_FLOAT32): rows the chunk summaries cannot settle, and the optional
+ * probabilities, read them from there.  Every other klsample_batch field means what it
+ * means for klsample_run; the workspace is sized by klsample_lmhead_workspace_size. */
+typedef struct klsample_lmhead {
+    const void *hidden;         /* [batch, dim] bf16, 16-byte aligned rows */
+    const void *weight;         /* [vocab, dim] bf16 (lm_head.weight), 16-byte aligned */
+    int32_t dim;                /* hidden size: a positive multiple of 32 */
+    int32_t reserved;           /* 0 */
+} klsample_lmhead;
+
+int klsample_lmhead_workspace_size(int32_t batch, int32_t vocab, int32_t max_top_k, int32_t num_logprobs,
+                                   size_t *bytes);
+int klsample_lmhead_run(const klsample_batch *batch, const klsample_lmhead *head, void *stream);
+
 /* Description of the last failure on this thread ("" if none). */
 const char *klsample_last_error(void);
 

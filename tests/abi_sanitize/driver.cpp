@@ -74,7 +74,7 @@ static klsample_batch make_batch(Bufs &b, int B, int V, int N, int32_t max_top_k
 }
 
 // every workspace region the launch received lies inside the workspace, 256-aligned
-static void check_plan(const Bufs &b, const klsample_batch &k) {
+static void check_plan(const Bufs &b, const klsample_batch &k, bool head = false) {
     const kls::Args &a = stub::last_args;
     const uintptr_t lo = (uintptr_t)k.workspace, hi = lo + k.workspace_bytes;
     auto inside = [&](const void *p, size_t n) {
@@ -93,7 +93,7 @@ static void check_plan(const Bufs &b, const klsample_batch &k) {
     const int kk = k.max_top_k < a.V ? k.max_top_k : a.V;
     const int want = 2 * (kk > 64 ? kk : 64) + 128;   // slots for the chunk's K best, capped at the chunk
     CHECK(a.cand_cap >= (want < a.C ? want : a.C) && a.cand_cap <= a.C && a.cand_cap % 64 == 0);
-    CHECK(a.wide_split == (BS <= (size_t)kls::kWideSplitGroups ? 1 : 0));
+    CHECK(a.wide_split == (!head && BS <= (size_t)kls::kWideSplitGroups ? 1 : 0));
     (void)b;
 }
 
@@ -198,6 +198,40 @@ int main() {
         k.options = KLSAMPLE_OPT_HISTORY_PAIRS;
         k.history_offsets = nullptr;
         expect_error(&k, KLSAMPLE_ERR_INVALID_ARGUMENT);
+    }
+
+    // the LM-head call: chunks of 1,024, one workgroup per chunk writes its histograms,
+    // the logits are the output; argument errors before any launch
+    {
+        Bufs b;
+        const int B = 5, V = 70001, N = 3, K = 50, d = 64;
+        klsample_batch k = make_batch(b, B, V, N, K);
+        size_t need = 0;
+        CHECK(klsample_lmhead_workspace_size(B, V, K, N, &need) == KLSAMPLE_OK);
+        b.ws.assign(need + 256, 0);
+        k.workspace = (void *)(((uintptr_t)b.ws.data() + 255) & ~(uintptr_t)255);
+        k.workspace_bytes = need;
+        alignas(16) static uint16_t hid[B * d], wt[V * d / 1000 + 64];
+        klsample_lmhead h = {hid, wt, d, 0};
+        const int before = stub::launches;
+        CHECK(klsample_lmhead_run(&k, &h, nullptr) == KLSAMPLE_OK && stub::launches == before + 1);
+        check_plan(b, k, true);
+        CHECK(stub::last_args.E == 4 && stub::last_args.C == 1024 && stub::last_args.wide_split == 0);
+        CHECK(stub::last_head.dim == d && stub::last_head.logits_out == (const float *)k.logits);
+        CHECK(klsample_lmhead_run(&k, nullptr, nullptr) == KLSAMPLE_ERR_INVALID_ARGUMENT);
+        klsample_lmhead e = h; e.dim = 48;
+        CHECK(klsample_lmhead_run(&k, &e, nullptr) == KLSAMPLE_ERR_INVALID_ARGUMENT);
+        e = h; e.weight = (const unsigned char *)wt + 2;
+        CHECK(klsample_lmhead_run(&k, &e, nullptr) == KLSAMPLE_ERR_INVALID_ARGUMENT);
+        e = h; e.hidden = nullptr;
+        CHECK(klsample_lmhead_run(&k, &e, nullptr) == KLSAMPLE_ERR_INVALID_ARGUMENT);
+        klsample_batch kb = k; kb.dtype = KLSAMPLE_BFLOAT16;
+        CHECK(klsample_lmhead_run(&kb, &h, nullptr) == KLSAMPLE_ERR_INVALID_ARGUMENT);
+        kb = k; kb.row_stride = V + 4;
+        CHECK(klsample_lmhead_run(&kb, &h, nullptr) == KLSAMPLE_ERR_INVALID_ARGUMENT);
+        kb = k; kb.workspace_bytes = need - 1;
+        CHECK(klsample_lmhead_run(&kb, &h, nullptr) == KLSAMPLE_ERR_WORKSPACE);
+        CHECK(stub::launches == before + 1);
     }
 
     // workspace init and phase events

@@ -8,6 +8,7 @@
 
 namespace stub {
 kls::Args last_args;
+kls::HeadArgs last_head;
 int launches = 0;
 int fills = 0;
 alignas(256) unsigned char scratch[1 << 16];
@@ -18,6 +19,13 @@ namespace kls {
 
 hipError_t launch_sample(const Args &a, int32_t, hipStream_t, const PhaseEvents *) {
     stub::last_args = a;
+    ++stub::launches;
+    return hipSuccess;
+}
+
+hipError_t launch_lmhead(const Args &a, const HeadArgs &h, hipStream_t) {
+    stub::last_args = a;
+    stub::last_head = h;
     ++stub::launches;
     return hipSuccess;
 }

@@ -4,6 +4,7 @@
 
 namespace stub {
 extern kls::Args last_args;
+extern kls::HeadArgs last_head;
 extern int launches;
 extern int fills;
 extern unsigned char scratch[];
