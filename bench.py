@@ -26,8 +26,11 @@ Printed on one JSON line:
 
 Other modes (used to produce the text summaries under ``profiles/``):
 
-* ``--profile-run``: only the headline steps and a 1 GiB copy that calibrates HBM
-  byte counters; meant to run under ``rocprofv3 --pmc``;
+* ``--profile-run [--workload NAME]``: only the steps of one workload (the headline by
+  default) and a 1 GiB copy that calibrates HBM byte counters; meant to run under
+  ``rocprofv3 --pmc``;
+* ``--lmhead``: the fused LM head + sampling call against a bf16 matmul followed by the
+  sampling call;
 * ``--summarize-stats DIR`` / ``--summarize-pmc FETCH_DIR WRITE_DIR``: turn the CSV
   output of rocprofv3 into those summaries;
 * ``--summarize-parity JSONL``: the per-case parity counts the GPU tests log.
@@ -544,6 +547,7 @@ def main():
     ap.add_argument('--cpu-seconds', type=float, default=12.0)
     ap.add_argument('--no-cpu-baseline', action='store_true')
     ap.add_argument('--profile-run', action='store_true')
+    ap.add_argument('--workload', default=None, help='workload of --profile-run (default: the headline)')
     ap.add_argument('--summarize-stats', metavar='DIR')
     ap.add_argument('--summarize-pmc', nargs=2, metavar=('FETCH_DIR', 'WRITE_DIR'))
     ap.add_argument('--summarize-parity', metavar='JSONL')
@@ -577,7 +581,8 @@ def main():
         return 0
 
     if args.profile_run:
-        res = Resident(HEADLINE, device)
+        name = args.workload or HEADLINE
+        res = Resident(name, device)
         for i in range(args.warmup + args.steps):
             res.launch(i)
         src = torch.empty(COPY_CALIBRATION_BYTES // 4, dtype=torch.float32, device=device).fill_(1.0)
@@ -585,7 +590,7 @@ def main():
         for _ in range(3):
             dst.copy_(src)
         torch.cuda.synchronize()
-        print(f'profile run: {args.warmup + args.steps} steps of {HEADLINE} and 3 copies of '
+        print(f'profile run: {args.warmup + args.steps} steps of {name} and 3 copies of '
               f'{COPY_CALIBRATION_BYTES >> 20} MiB', flush=True)
         return 0
 

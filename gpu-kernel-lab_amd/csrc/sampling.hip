@@ -1698,20 +1698,26 @@ __device__ __forceinline__ bool wide_resolve(const Args &a, int row, const klsam
         return ((unsigned long long)(uint32_t)hi << 32) | (uint32_t)lo;
     };
     // 1. merge: thread t reads words t, t + 256, ... of the row's chunk histograms
-    //    (chunk c = word >> 10), sixteen loads in flight
+    //    (chunk c = word >> 10; each bin the difference of two prefix words), sixteen
+    //    pairs of loads in flight
     static_assert(kWideBins == 1024, "chunk index = word >> 10");
     const int nw = S * kWideBins;
     for (int q0 = 0; q0 < nw; q0 += 16 * kThreads) {
-        unsigned long long v[16];
+        unsigned long long v[16], pv[16];
 #pragma unroll
-        for (int u = 0; u < 16; ++u) v[u] = hist[min(q0 + u * kThreads + tid, nw - 1)];
+        for (int u = 0; u < 16; ++u) {
+            const int q = min(q0 + u * kThreads + tid, nw - 1);
+            v[u] = hist[q];
+            pv[u] = hist[(q & (kWideBins - 1)) ? q - 1 : q];
+        }
 #pragma unroll
         for (int u = 0; u < 16; ++u) {
             const int q = q0 + u * kThreads + tid;
-            if (q < nw && v[u] != 0ull) {
+            const unsigned long long d = (q & (kWideBins - 1)) ? v[u] - pv[u] : v[u];
+            if (q < nw && d != 0ull) {
                 const int c = q >> 10, j = min((q & (kWideBins - 1)) + cd[c], kWideBins - 1);
-                atomicAdd(&hc[j], (uint32_t)(v[u] >> kWideCountShift));
-                atomicAdd(&hm[j], conv(v[u], c));
+                atomicAdd(&hc[j], (uint32_t)(d >> kWideCountShift));
+                atomicAdd(&hm[j], conv(d, c));
             }
         }
     }
@@ -1753,22 +1759,10 @@ __device__ __forceinline__ bool wide_resolve(const Args &a, int row, const klsam
     if (!ms.flag || bstar == kWideBins - 1 || nb < 1) return false;
     const unsigned long long above = ms.sel_above_mass;
     const uint32_t above_count = ms.sel_above_count;
-    // 3. per chunk: the mass of its bins above the cut bin; sixteen loads in flight, the
-    //    256 words of one load round all of one chunk (a wave sum, one LDS atomic)
-    static_assert(kWideBins % kThreads == 0, "a load round stays within one chunk");
-    for (int q0 = 0; q0 < nw; q0 += 16 * kThreads) {
-        unsigned long long v[16];
-#pragma unroll
-        for (int u = 0; u < 16; ++u) v[u] = hist[min(q0 + u * kThreads + tid, nw - 1)];
-#pragma unroll
-        for (int u = 0; u < 16; ++u) {
-            const int qr = q0 + u * kThreads;   // (uniform)
-            if (qr >= nw) break;
-            const int c = qr >> 10, jc = (qr + tid) & (kWideBins - 1);
-            unsigned long long msum = (v[u] != 0ull && jc + cd[c] < bstar) ? conv(v[u], c) : 0ull;
-            msum = wave_reduce(msum, OpSumQ(), 0ull);
-            if (lane_id() == 0 && msum) atomicAdd(&kc[c], msum);
-        }
+    // 3. per chunk: the mass of its bins above the cut bin, one prefix word
+    for (int c = tid; c < S; c += kThreads) {
+        const int nc = min(kWideBins, bstar - cd[c]);
+        kc[c] = nc > 0 ? conv(hist[(size_t)c * kWideBins + nc - 1], c) : 0ull;
     }
     if (tid == 0) ms.ncand = 0;
     for (int i = tid; i < 256; i += kThreads) { ms.hist[i] = 0u; ms.hmass[i] = 0ull; }
@@ -1811,15 +1805,68 @@ __device__ __forceinline__ bool wide_resolve(const Args &a, int row, const klsam
             for (int u = 0; u < U; ++u) qa[u] = qb[u];
         }
     };
-    each_cut([&](float y, int idx) {
-        const int sb = sub(y);
-        atomicAdd(&ms.hist[sb], 1u);
-        atomicAdd(&ms.hmass[sb], weight_fix(y, m));
-        if (listed) {
-            const int pos = wave_append(&ms.ncand);
-            if (pos < kWideList) L[pos] = desc_key(y, idx);
+    if (listed) {
+        // The pass only lists the entries' indices: a lane marks its hits of a load
+        // round in a 64-bit mask, and the wave reserves the round's list slots with one
+        // atomic (the entries are sparse: anything done per entry inside the pass would
+        // run with one or two lanes active and wait on LDS each time).  Their scores,
+        // sub-bin counts and masses are then taken from the list with every lane busy.
+        constexpr int U = 16;
+        const int n4 = (V + 3) / 4;   // the buffer is readable up to V rounded up to 4
+        const float4 *y4 = reinterpret_cast<const float4 *>(yb);
+        float4 qa[U], qb[U];
+        auto request = [&](float4 (&q)[U], int b0) {
+#pragma unroll
+            for (int u = 0; u < U; ++u) q[u] = y4[min(b0 + u * kThreads + tid, n4 - 1)];
+        };
+        request(qa, 0);
+        for (int b0 = 0; b0 < n4; b0 += U * kThreads) {
+            request(qb, b0 + U * kThreads);
+            unsigned long long mask = 0ull;
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const float t[4] = {qa[u].x, qa[u].y, qa[u].z, qa[u].w};
+                const int vi = b0 + u * kThreads + tid;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const bool hit = t[e] >= lo_b && t[e] < hi_b && 4 * vi + e < V && vi < n4;
+                    mask |= (unsigned long long)hit << (4 * u + e);
+                }
+            }
+            const uint32_t cnt = (uint32_t)__popcll(mask);
+            const uint32_t incl = wave_incl_scan(cnt);
+            const uint32_t total = readlane(incl, 63);
+            if (total) {
+                int base = 0;
+                if (lane_id() == 0) base = atomicAdd(&ms.ncand, (int)total);
+                int pos = __builtin_amdgcn_readfirstlane(base) + (int)(incl - cnt);
+                while (mask) {
+                    const int bit = __builtin_ctzll(mask);
+                    mask &= mask - 1ull;
+                    if (pos < kWideList) L[pos] = (unsigned long long)(4 * (b0 + (bit >> 2) * kThreads + tid) + (bit & 3));
+                    ++pos;
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < U; ++u) qa[u] = qb[u];
         }
-    });
+        __syncthreads();
+        const int nl = min(ms.ncand, kWideList);
+        for (int i = tid; i < nl; i += kThreads) {
+            const int idx = (int)L[i];
+            const float y = yb[idx];
+            L[i] = desc_key(y, idx);
+            const int sb = sub(y);
+            atomicAdd(&ms.hist[sb], 1u);
+            atomicAdd(&ms.hmass[sb], weight_fix(y, m));
+        }
+    } else {
+        each_cut([&](float y, int idx) {
+            const int sb = sub(y);
+            atomicAdd(&ms.hist[sb], 1u);
+            atomicAdd(&ms.hmass[sb], weight_fix(y, m));
+        });
+    }
     __syncthreads();
     if (listed && ms.ncand != nb) return false;   // (the histogram and the scores always agree)
     if (wave_id() == 0) {
@@ -3102,7 +3149,7 @@ struct ScanLds {
     static constexpr int mask_off = stage_off + kWaves * kStageLanes * stride * 4;
     static constexpr int penalty = mask_off + kThreads * 4;
     static constexpr int keys = kThreads * (E < 16 ? E : 16) * 4;   // fallback bound (later)
-    static constexpr int wide = kWideBins * 8;                       // top-p chunk histogram (last)
+    static constexpr int wide = kWideBins * 8 + 64;                  // top-p chunk histogram (last)
     static constexpr int value0 = penalty > keys ? penalty : keys;
     static constexpr int value = value0 > wide ? value0 : wide;
 };
@@ -3111,9 +3158,12 @@ struct ScanLds {
 // floor(y * kWideCells) with G = floor(mc * kWideCells), capped at the last bin (see
 // internal.h); each histogram word adds 1 at bit kWideCountShift and the entry's weight
 // exp(y - G / kWideCells) in units of 2^-kWideMassBits below it (integer sums: exact
-// and independent of their order).  The scores go to the row's score buffer in vocab
-// order (16-byte stores).  x holds the chunk's final scores, -inf past its end.  `raw`
-// holds kWideBins * 8 bytes of free LDS.
+// and independent of their order).  The words are stored as an inclusive prefix over
+// the bins (word j: bins 0..j; the packed count and mass add together, the chunk's
+// totals staying below their fields' limits), so that the mass above any bin is one
+// load.  The scores go to the row's score buffer in vocab order (16-byte stores).  x
+// holds the chunk's final scores, -inf past its end.  `raw` holds kWideBins * 8 + 64
+// bytes of free LDS.
 template <typename TIn, int E>
 __device__ __forceinline__ void wide_chunk(const Args &a, int row, int chunk, const float (&x)[E], float mc,
                                            unsigned char *raw) {
@@ -3155,8 +3205,21 @@ __device__ __forceinline__ void wide_chunk(const Args &a, int row, int chunk, co
         }
     }
     __syncthreads();
-    uint4 *gh = reinterpret_cast<uint4 *>(a.hist + ((size_t)row * a.S + chunk) * kWideBins);
-    for (int i = tid; i < kWideBins / 2; i += kThreads) gh[i] = h4[i];
+    // inclusive prefix: four consecutive bins per thread, then across threads
+    static_assert(kWideBins == 4 * kThreads, "four bins per thread");
+    unsigned long long w4[4], run = 0ull;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) { run += hb[4 * tid + k]; w4[k] = run; }
+    const unsigned long long incl = wave_incl_scan(run);
+    unsigned long long *wt = hb + kWideBins;   // the four waves' totals
+    if (lane_id() == 63) wt[wave_id()] = incl;
+    __syncthreads();
+    unsigned long long off = incl - run;
+    for (int w = 0; w < wave_id(); ++w) off += wt[w];
+    uint4 *gh = reinterpret_cast<uint4 *>(a.hist + ((size_t)row * a.S + chunk) * kWideBins) + 2 * tid;
+    const unsigned long long o0 = w4[0] + off, o1 = w4[1] + off, o2 = w4[2] + off, o3 = w4[3] + off;
+    gh[0] = make_uint4((uint32_t)o0, (uint32_t)(o0 >> 32), (uint32_t)o1, (uint32_t)(o1 >> 32));
+    gh[1] = make_uint4((uint32_t)o2, (uint32_t)(o2 >> 32), (uint32_t)o3, (uint32_t)(o3 >> 32));
 }
 
 // Streaming pass: one workgroup per (row, chunk).  The LDS footprint (~26 KB at 32
