@@ -124,7 +124,11 @@ int klsample_abi_version(void);
 
 /* Bytes of device workspace a call with these sizes needs.  Writes *bytes and
  * returns KLSAMPLE_OK, or a negative status for invalid sizes.
- * No reference counterpart: the reference allocates inside torch ops per call. */
+ * No reference counterpart: the reference allocates inside torch ops per call.
+ * The size grows with batch * vocab: per row a score buffer of vocab + 1 floats
+ * (rounded up to 4) and 8 KB per chunk of 8,192 entries for top-p histograms, next to
+ * the chunk summaries and candidate slots (the headline B = 256, V = 151,936 needs
+ * ~200 MB; B = 1,024 ~800 MB).  Callers bounding their workspace split the batch. */
 int klsample_workspace_size(int32_t batch, int32_t vocab, int32_t dtype, int32_t max_top_k,
                             int32_t num_logprobs, size_t *bytes);
 
