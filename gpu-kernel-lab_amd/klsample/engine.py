@@ -102,9 +102,9 @@ class DeviceHistory:
     def slots(self, rids) -> np.ndarray:
         return np.fromiter((self.slot[r] for r in rids), dtype=np.int64, count=len(rids))
 
-    def prepare(self, slots: np.ndarray) -> np.ndarray:
+    def prepare(self, slots: np.ndarray, out: np.ndarray | None = None) -> np.ndarray:
         """Room for one more token in each of these requests; their ``[begin, end)``
-        ranges as the library's history pairs (int32, 2 per row)."""
+        ranges as the library's history pairs (int32, 2 per row), in ``out`` if given."""
         full = slots[self.length[slots] >= self.cap[slots]]
         for s in full.tolist():
             start, length, cap = int(self.start[s]), int(self.length[s]), int(self.cap[s])
@@ -112,7 +112,8 @@ class DeviceHistory:
             self.arena[new_start:new_start + length].copy_(self.arena[start:start + length])
             self.free_segments.append((start, cap))
             self.start[s], self.cap[s] = new_start, 2 * cap
-        out = np.empty(2 * slots.size, dtype=np.int32)
+        if out is None or out.size != 2 * slots.size:
+            out = np.empty(2 * slots.size, dtype=np.int32)
         out[0::2] = self.start[slots]
         out[1::2] = self.start[slots] + self.length[slots]
         return out
@@ -229,6 +230,7 @@ class BatchedStep:
         self.counts = [min(s.params.logprobs, V, self.N) for s in samplers]
         self.stop_rows = [(b, s.params.stop_token_ids) for b, s in enumerate(samplers) if s.params.stop_token_ids]
         self.slots = self.history.slots(rids) if self.history is not None else None
+        self.ranges = np.empty(2 * len(rids), dtype=np.int32)
 
     def run(self, rids, samplers, logits: torch.Tensor) -> StepOutput:
         if logits.dim() != 2 or not logits.is_floating_point():
@@ -252,7 +254,7 @@ class BatchedStep:
             rows['uniform'][self.sampled_idx] = self.U[self.ar, self.pos]
             self.pos += 1
         if hist is not None:
-            ranges = hist.prepare(self.slots)
+            ranges = hist.prepare(self.slots, self.ranges)
             arena = hist.arena.data_ptr()
             out = self.runner.run_packed(logits, rows, self.max_top_k, N, offsets=ranges, ids_ptr=arena,
                                          append_ptr=arena, options=_lib.OPT_HISTORY_PAIRS)

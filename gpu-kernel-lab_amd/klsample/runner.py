@@ -124,6 +124,7 @@ class DeviceRunner:
         self.index = self.device.index if self.device.index is not None else torch.cuda.current_device()
         self.lib = _lib.load()
         self.layouts = {}        # call shape -> record and output views (see _layout)
+        self.pointers = {}       # id(host array) -> (array, address): arrays handed over repeatedly
         self.generation = 0      # bumped whenever a buffer is replaced
         self.workspace = None
         self.workspace_bytes = 0
@@ -138,6 +139,7 @@ class DeviceRunner:
             return
         nbytes = _align(max(nbytes, int(self.workspace_bytes * 1.25)), 1 << 20)
         self.generation += 1
+        self.layouts.clear()   # (they point into the buffers being replaced)
         with torch.inference_mode(False):   # ordinary tensors: writable in and out of inference mode
             ws = torch.empty(nbytes + 256, dtype=torch.uint8, device=self.device)
         base = ws.data_ptr()
@@ -161,6 +163,7 @@ class DeviceRunner:
             return
         n = _align(max(nbytes, 4096), 4096)
         self.generation += 1
+        self.layouts.clear()
         with torch.inference_mode(False):
             self.out_host = torch.empty(n, dtype=torch.uint8, pin_memory=True)
             # the kernels write the outputs straight into this pinned buffer when the
@@ -224,6 +227,14 @@ class DeviceRunner:
         self.layouts[key] = lay
         return lay
 
+    def _address(self, arr: np.ndarray) -> int:
+        hit = self.pointers.get(id(arr))
+        if hit is None or hit[0] is not arr:
+            if len(self.pointers) > 4096:
+                self.pointers.clear()
+            hit = self.pointers[id(arr)] = (arr, arr.ctypes.data)
+        return hit[1]
+
     def _stream(self) -> int:
         return torch._C._cuda_getCurrentRawStream(self.index)
 
@@ -281,8 +292,8 @@ class DeviceRunner:
             self.stage_dev[:stage_bytes].copy_(self.stage_host[:stage_bytes], non_blocking=True)
             dbase = self.stage_dev.data_ptr()
         if host_params:
-            batch.params = rows.ctypes.data
-            batch.history_offsets = offsets.ctypes.data if offsets is not None else None
+            batch.params = self._address(rows)
+            batch.history_offsets = self._address(offsets) if offsets is not None else None
         else:
             batch.params = dbase
             batch.history_offsets = dbase + o_off if offsets is not None else None
