@@ -2688,6 +2688,32 @@ __device__ __forceinline__ bool combine_row(const Args &a, int row, const klsamp
         }
     }
 
+    // A greedy row with no top-N list needs nothing but the summaries: argmax, and the
+    // max and sum-exp of its logprob.
+    if (mode == kGreedy && N == 0) {
+        arg = wave_reduce(arg, OpMinI(), 0x7fffffff);
+        Z = wave_reduce(Z, OpSumD(), 0.0);
+        if (lane_id() == 0) {
+            ms.red.d[wave_id()] = Z;
+            atomicMin(&ms.ia, arg);
+        }
+        __syncthreads();
+        Z = ms.red.d[0];
+#pragma unroll
+        for (int w = 1; w < kWaves; ++w) Z += ms.red.d[w];
+        RowOut r;
+        r.path = 0;
+        r.m = m;
+        r.cut = kNegInf;
+        r.cut_idx = V;
+        r.kept = nfinite;
+        r.log_norm = log(Z);
+        r.token = (ms.ia == 0x7fffffff) ? 0 : ms.ia;
+        r.logprob = -r.log_norm;
+        emit_row(a, row, mode, r, reinterpret_cast<unsigned long long *>(raw) + kSortCap, 0, ms);
+        return true;
+    }
+
     // 3. F = { candidates >= lo } into A; every element of the row scoring >= lo is in
     //    it.  Its key range is tracked for the selection.  Top-k rows keep their
     //    candidates' scores before the division by T (the order is the same): they are
