@@ -195,3 +195,16 @@ def test_uniforms_taken_in_blocks_and_returned_keep_the_stream():
     got += blk.tolist()
     got += [s.next_uniform('cpu') for _ in range(10)]
     assert got == want[:len(got)]
+
+
+def test_smoke_report_reads_the_parity_report():
+    """smoke() prints its line from the same report the GPU tests build; a failing report
+    raises."""
+    import __graft_entry__ as entry
+    from helpers import ParityReport
+    rep = ParityReport(rows=2, greedy=1, sampled=1, exact=2)
+    line = entry.smoke_report(np.array([3, 4]), rep)
+    assert line.startswith('smoke ok: tokens=[3, 4]') and "'exact': 2" in line
+    rep.failures.append('row 0: token 1 != oracle 2')
+    with pytest.raises(AssertionError):
+        entry.smoke_report(np.array([1]), rep)
