@@ -256,8 +256,8 @@ int klsample_lmhead_run(const klsample_batch *b, const klsample_lmhead *h, void 
     if (h == nullptr) return fail(KLSAMPLE_ERR_INVALID_ARGUMENT, "head must not be NULL");
     if (h->hidden == nullptr || h->weight == nullptr)
         return fail(KLSAMPLE_ERR_INVALID_ARGUMENT, "hidden and weight must not be NULL");
-    if (h->dim < 32 || h->dim % 32 != 0)
-        return fail(KLSAMPLE_ERR_INVALID_ARGUMENT, "dim (%d) must be a positive multiple of 32", h->dim);
+    if (h->dim < 64 || h->dim % 64 != 0)
+        return fail(KLSAMPLE_ERR_INVALID_ARGUMENT, "dim (%d) must be a positive multiple of 64", h->dim);
     if ((((uintptr_t)h->hidden | (uintptr_t)h->weight) & 15u) != 0)
         return fail(KLSAMPLE_ERR_INVALID_ARGUMENT, "hidden and weight must be 16-byte aligned");
     if (b != nullptr && (b->dtype != KLSAMPLE_FLOAT32 || b->row_stride != b->vocab))

@@ -124,7 +124,7 @@ struct HeadArgs {
     const uint16_t *hidden;   // [B][dim] bf16
     const uint16_t *weight;   // [V][dim] bf16
     float *logits_out;        // [B][V] fp32
-    int32_t dim;              // multiple of 32
+    int32_t dim;              // multiple of 64
 };
 hipError_t launch_lmhead(const Args &args, const HeadArgs &head, hipStream_t stream);
 hipError_t launch_zero_fill(void *ptr, size_t bytes, hipStream_t stream);

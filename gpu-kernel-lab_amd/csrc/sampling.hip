@@ -3788,29 +3788,33 @@ __global__ __launch_bounds__(kThreads) void lmhead_kernel(Args a, HeadArgs h) {
         const int v = vwave + t * 16 + n;
         wrow[t] = h.weight + (size_t)(v < a.V ? v : 0) * h.dim + 8 * g;
     }
-    const bool hvalid = r0 + n < a.B;
-    const uint16_t *hrow = h.hidden + (size_t)(hvalid ? r0 + n : 0) * h.dim + 8 * g;
+    // (rows past B repeat the block's last row: their products are neither scanned nor
+    // written, and the loads stay unconditional)
+    const uint16_t *hrow = h.hidden + (size_t)min(r0 + n, a.B - 1) * h.dim + 8 * g;
     f32x4 acc[kTiles];
 #pragma unroll
     for (int t = 0; t < kTiles; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-    const bf16x8 zero8 = {};
-    bf16x8 an[kTiles], bn;
+    // Two operand sets take turns, each reloaded two steps ahead right after its products
+    // are issued: two steps of loads stay in flight.  Every load is unconditional (the
+    // offsets clamp to the last step, dim being a multiple of 64), so that the waits
+    // before the products count only the loads they need.
+    bf16x8 ax[kTiles], ay[kTiles], bx, by;
+    auto load = [&](bf16x8 (&av)[kTiles], bf16x8 &bv, int k) {
+        k = min(k, h.dim - 32);
 #pragma unroll
-    for (int t = 0; t < kTiles; ++t) an[t] = __builtin_nontemporal_load(reinterpret_cast<const bf16x8 *>(wrow[t]));
-    bn = hvalid ? *reinterpret_cast<const bf16x8 *>(hrow) : zero8;
-    for (int k0 = 0; k0 < h.dim; k0 += 32) {
-        bf16x8 ac[kTiles];
+        for (int t = 0; t < kTiles; ++t) av[t] = *reinterpret_cast<const bf16x8 *>(wrow[t] + k);
+        bv = *reinterpret_cast<const bf16x8 *>(hrow + k);
+        __builtin_amdgcn_sched_barrier(0);   // the loads stay here, ahead of the products that need them
+    };
+    load(ax, bx, 0);
+    load(ay, by, 32);
+    for (int k0 = 0; k0 < h.dim; k0 += 64) {
 #pragma unroll
-        for (int t = 0; t < kTiles; ++t) ac[t] = an[t];
-        const bf16x8 bc = bn;
-        if (k0 + 32 < h.dim) {
+        for (int t = 0; t < kTiles; ++t) acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ax[t], bx, acc[t], 0, 0, 0);
+        load(ax, bx, k0 + 64);
 #pragma unroll
-            for (int t = 0; t < kTiles; ++t)
-                an[t] = __builtin_nontemporal_load(reinterpret_cast<const bf16x8 *>(wrow[t] + k0 + 32));
-            bn = hvalid ? *reinterpret_cast<const bf16x8 *>(hrow + k0 + 32) : zero8;
-        }
-#pragma unroll
-        for (int t = 0; t < kTiles; ++t) acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ac[t], bc, acc[t], 0, 0, 0);
+        for (int t = 0; t < kTiles; ++t) acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ay[t], by, acc[t], 0, 0, 0);
+        load(ay, by, k0 + 96);
     }
     // tile t, lane l, entry j: vocabulary row vwave + 16t + 4g + j, batch row r0 + n
     const int rowg = r0 + n;

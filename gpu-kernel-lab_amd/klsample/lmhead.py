@@ -21,7 +21,7 @@ def lmhead_sample(hidden: torch.Tensor, weight: torch.Tensor, params_list, histo
     """Sample one token per row of ``hidden @ weight.T``.
 
     ``hidden`` is ``[B, d]`` bf16 and ``weight`` ``[V, d]`` bf16 (``lm_head.weight``),
-    both contiguous on one GPU, ``d`` a multiple of 32.  Rows take ``params_list``,
+    both contiguous on one GPU, ``d`` a multiple of 64.  Rows take ``params_list``,
     ``histories`` and ``uniforms`` as in ``sample_batch``.  Returns the batch output and
     the ``[B, V]`` fp32 logits (bf16-rounded values)."""
     if hidden.dim() != 2 or weight.dim() != 2 or hidden.shape[1] != weight.shape[1]:

@@ -181,7 +181,7 @@ int klsample_set_phase_events(void *const *events, int32_t count);
 typedef struct klsample_lmhead {
     const void *hidden;         /* [batch, dim] bf16, 16-byte aligned rows */
     const void *weight;         /* [vocab, dim] bf16 (lm_head.weight), 16-byte aligned */
-    int32_t dim;                /* hidden size: a positive multiple of 32 */
+    int32_t dim;                /* hidden size: a positive multiple of 64 */
     int32_t reserved;           /* 0 */
 } klsample_lmhead;
 

@@ -86,7 +86,7 @@ def test_fused_lm_head_matches_the_product_and_the_oracle(B, V, d, seed, greedy_
 
 
 def test_fused_lm_head_argument_errors():
-    h = torch.zeros(2, 48, dtype=torch.bfloat16, device=DEV)     # dim not a multiple of 32
+    h = torch.zeros(2, 48, dtype=torch.bfloat16, device=DEV)     # dim not a multiple of 64
     w = torch.zeros(100, 48, dtype=torch.bfloat16, device=DEV)
     from klsample._lib import KLSampleError
     with pytest.raises((ValueError, KLSampleError)):
