@@ -2618,6 +2618,77 @@ __device__ __forceinline__ void request_row(const Args &a, int row, RowSpec &r) 
 // Resolve one row from its chunk summaries and candidates.  Runs in one workgroup of
 // kThreads.  Returns false when the candidates cannot settle the row (the caller then
 // runs dense_resolve).
+// finish_list for lists of at most kThreads entries: the whole list sorted once (block
+// rank sort), the top-p cut taken in it directly and the draw made over its kept
+// prefix in vocab order; the same decisions as finish_list (the same fixed-point
+// weights relative to the list's best score, the reference's exclusive rule within the
+// crossing group of equal scores, the same rounding fallbacks), with fewer block phases.
+// E[0..n) unsorted keys (n <= kThreads); W holds 2 * kThreads keys of scratch.
+__device__ __forceinline__ bool finish_small(const Args &a, int row, int mode, const klsample_row_params &p,
+                                             const unsigned long long *E, int n, bool topp, double zrow,
+                                             bool complete, unsigned long long *W, Misc &ms) {
+    const int V = a.V, N = a.N, tid = threadIdx.x;
+    for (int i = tid; i < n; i += kThreads) W[i] = E[i];
+    __syncthreads();
+    if (n > 1) block_rank_sort(W, n, ms.part);
+    __syncthreads();
+    const float mref = desc_key_y(W[0]), ylo = desc_key_y(W[n - 1]);
+    const unsigned long long zall = block_sumq(tid < n ? weight_fix(desc_key_y(W[tid]), mref) : 0ull, ms);
+    TopPCut tc;
+    bool cut_all = true;   // every entry kept
+    if (topp) {
+        const double target = (double)p.top_p * (zrow >= 0.0 ? zrow : (double)zall);
+        if ((double)zall > target) {   // some entry's inclusive mass exceeds the target
+            cut_in_sorted(W, n, 0ull, 0u, target, mref, tc, ms);
+            cut_all = false;
+        } else if (!complete) {
+            return false;   // the kept mass reaches past the list
+        }
+    }
+    const float cut = cut_all ? ylo : tc.cut;
+    const int cut_idx = (cut_all || tc.cut_idx == 0x7fffffff) ? V : tc.cut_idx;
+    const int kept_n = cut_all ? n : tc.kept;
+    const unsigned long long zf = cut_all ? zall : tc.zf;
+    // the kept prefix in vocab order, then the first entry whose inclusive mass exceeds
+    // u * kept mass (the last one if rounding leaves it short)
+    unsigned long long *X = W + kThreads;
+    for (int i = tid; i < kept_n; i += kThreads)
+        X[i] = ((unsigned long long)(uint32_t)desc_key_idx(W[i]) << 32) | __float_as_uint(desc_key_y(W[i]));
+    __syncthreads();
+    if (kept_n > 1) block_rank_sort(X, kept_n, ms.part);
+    __syncthreads();
+    const unsigned long long tgt = (unsigned long long)floor((double)p.uniform * (double)zf);
+    if (wave_id() == 0) {
+        const int l = lane_id();
+        unsigned long long run = 0ull;
+        int found = -1;
+        for (int i0 = 0; i0 < kept_n && found < 0; i0 += 64) {
+            const int i = i0 + l;
+            const unsigned long long w = i < kept_n ? weight_fix(__uint_as_float((uint32_t)X[i]), mref) : 0ull;
+            const unsigned long long incl = run + wave_incl_scan(w);
+            const unsigned long long bal = __ballot(i < kept_n && incl > tgt);
+            if (bal) found = i0 + __ffsll((long long)bal) - 1;
+            run = readlane(incl, 63);
+        }
+        if (found < 0) found = max(kept_n - 1, 0);
+        if (l == 0) ms.ia = found;
+    }
+    __syncthreads();
+    const unsigned long long kt = X[ms.ia];
+    RowOut r;
+    r.token = (int)(kt >> 32);
+    r.m = mref;
+    r.cut = cut;
+    r.cut_idx = cut_idx;
+    r.kept = kept_n;
+    r.log_norm = log((double)zf / kFixScale);
+    r.logprob = (double)__uint_as_float((uint32_t)kt) - (double)mref - r.log_norm;
+    r.path = 0;
+    __syncthreads();
+    emit_row(a, row, mode, r, W, min(N, kept_n), ms);   // the top-N: the sorted list's first entries
+    return true;
+}
+
 template <typename TIn, int E>
 __device__ __forceinline__ bool combine_row(const Args &a, int row, const klsample_row_params &p, int mode,
                                             const RowSpec &rs, unsigned char *raw, int *cnt, Misc &ms) {
@@ -3068,7 +3139,10 @@ __device__ __forceinline__ bool combine_row(const Args &a, int row, const klsamp
             __syncthreads();
             if (small) sort_top(D, lk, ms);
         }
-        if (!small) return finish_list(a, row, mode, p, D, lk, topp, -1.0, true, A, ms);
+        if (!small) {
+            if (lk <= kThreads) return finish_small(a, row, mode, p, D, lk, topp, -1.0, true, A, ms);
+            return finish_list(a, row, mode, p, D, lk, topp, -1.0, true, A, ms);
+        }
         const double mref = (double)desc_key_y(D[0]);
         if (wave_id() == 0) {
             int L = lk;
