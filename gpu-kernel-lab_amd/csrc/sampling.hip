@@ -2794,13 +2794,6 @@ __device__ __forceinline__ bool combine_row(const Args &a, int row, const klsamp
     unsigned long long *D = A + kSortCap;
     const float xs = (mode == kTopK) ? quotient_threshold(lo, p.temperature) : lo;
     uint32_t kmin = 0xffffffffu, kmax = 0u;
-    auto take = [&](float y, int idx) {
-        const int pos = wave_append(&ms.ncand);
-        if (pos < kSortCap) A[pos] = desc_key(y, idx);
-        const uint32_t k = fkey(y);
-        kmin = min(kmin, k);
-        kmax = max(kmax, k);
-    };
     {
         // the requested slots: accepted ones counted first, one LDS atomic per wave
         // reserves their places, then they are written
@@ -2844,12 +2837,55 @@ __device__ __forceinline__ bool combine_row(const Args &a, int row, const klsamp
         }
     }
     if (need_rest) {
-        // the rest: chunks beyond the requested ones, and slots past the requested pairs
+        // the rest: chunks beyond the requested ones, and slots past the requested pairs.
+        // Top-k rows: while more than 128 remain, eight slots per lane are requested at once
+        // (clamped addresses), the accepted ones counted and their places reserved with one
+        // LDS atomic per wave; the last ones (and every slot of other rows) are taken one
+        // slot per lane at a time.
+        const int l = lane_id();
+        unsigned long long *const sink = &ms.sink[tid];
+        auto visit = [&](auto width, const uint2 *pc, int j0, int nc) {
+            constexpr int U = decltype(width)::value;
+            uint2 e[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u) e[u] = pc[min(j0 + u * 64 + l, nc - 1)];
+            uint32_t acc = 0u;
+#pragma unroll
+            for (int u = 0; u < U; ++u)
+                if (j0 + u * 64 + l < nc && __uint_as_float(e[u].x) >= xs) acc |= 1u << u;
+            if (__ballot(acc != 0u) == 0ull) return;   // none accepted: nothing to store
+            const int mine = __popc(acc);
+            const int incl = wave_incl_scan(mine);
+            int base = 0;
+            if (l == 63) base = atomicAdd(&ms.ncand, incl);
+            base = readlane(base, 63) + incl - mine;
+#pragma unroll
+            for (int u = 0; u < U; ++u) {   // branch-free, as for the requested slots
+                const bool ok = (acc >> u) & 1u;
+                const float y = __uint_as_float(e[u].x);
+                *((ok && base < kSortCap) ? &A[base] : sink) = desc_key(y, (int)e[u].y);
+                base += ok ? 1 : 0;
+                const uint32_t k = fkey(y);
+                kmin = ok ? min(kmin, k) : kmin;
+                kmax = ok ? max(kmax, k) : kmax;
+            }
+        };
         for (int c = wave_id(); c < S; c += kWaves) {
             const int nc = cnt[c];
-            for (int j = (c < nspec ? 2 * ppc : 0) + lane_id(); j < nc; j += 64) {
-                const Cand cd = rc[(size_t)c * a.cand_cap + j];
-                if (cd.y >= xs) take(cd.y, cd.idx);
+            const uint2 *pc = reinterpret_cast<const uint2 *>(rc + (size_t)c * a.cand_cap);
+            int j0 = (c < nspec ? 2 * ppc : 0);
+            if (mode == kTopK)
+                for (; nc - j0 > 128; j0 += 512) visit(std::integral_constant<int, 8>{}, pc, j0, nc);
+            for (int j = j0 + l; j < nc; j += 64) {   // the last 128 or fewer, one slot at a time
+                const uint2 cd = pc[j];
+                const float y = __uint_as_float(cd.x);
+                if (y >= xs) {
+                    const int pos = wave_append(&ms.ncand);
+                    if (pos < kSortCap) A[pos] = desc_key(y, (int)cd.y);
+                    const uint32_t k = fkey(y);
+                    kmin = min(kmin, k);
+                    kmax = max(kmax, k);
+                }
             }
         }
     }
